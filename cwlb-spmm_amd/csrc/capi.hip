@@ -1,0 +1,315 @@
+// C ABI of libcwlb: contexts, errors and the SpMM entry points.
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "internal.h"
+
+namespace cwlb {
+
+namespace {
+thread_local std::string g_last_error;
+}
+
+void set_error(const std::string& msg) { g_last_error = msg; }
+
+cwlb_status fail(cwlb_status st, const std::string& msg)
+{
+    set_error(msg);
+    return st;
+}
+
+cwlb_status hip_fail(hipError_t e, const char* what)
+{
+    set_error(std::string(what) + ": " + hipGetErrorString(e));
+    return e == hipErrorOutOfMemory ? CWLB_OOM : CWLB_HIP_ERROR;
+}
+
+namespace {
+
+cwlb_status check_spmm_args(cwlb_ctx* ctx, const SpmmArgs& a)
+{
+    if (!ctx) return fail(CWLB_INVALID_ARG, "spmm: null context");
+    if (a.n_rows < 0 || a.nnz < 0 || a.K < 0 || a.n_tasks < 0 || a.h_rows < 0)
+        return fail(CWLB_INVALID_ARG, "spmm: negative size");
+    if (a.nnz > INT32_MAX) return fail(CWLB_INVALID_ARG, "spmm: nnz must fit int32");
+    const bool work = a.K > 0 && a.n_tasks > 0;
+    if (work) {
+        if (!a.row_ptr || !a.origin || !a.tasks || !a.C)
+            return fail(CWLB_INVALID_ARG, "spmm: null device pointer");
+        if (a.nnz > 0 && (!a.col_idx || !a.val || !a.H))
+            return fail(CWLB_INVALID_ARG, "spmm: null device pointer");
+    }
+    if (a.n_rows > 0 && a.K > 0 && !a.C) return fail(CWLB_INVALID_ARG, "spmm: null C");
+    return CWLB_OK;
+}
+
+cwlb_status finish_timed(cwlb_ctx* ctx, cwlb_timing* timing)
+{
+    CWLB_HIP_TRY(hipEventSynchronize(ctx->ev[2]));
+    float z = 0.0f, m = 0.0f;
+    CWLB_HIP_TRY(hipEventElapsedTime(&z, ctx->ev[0], ctx->ev[1]));
+    CWLB_HIP_TRY(hipEventElapsedTime(&m, ctx->ev[1], ctx->ev[2]));
+    timing->zero_us = z * 1000.0f;
+    timing->main_us = m * 1000.0f;
+    timing->total_us = (z + m) * 1000.0f;
+    int st = 0;
+    CWLB_HIP_TRY(hipMemcpy(&st, ctx->d_status, sizeof(int), hipMemcpyDeviceToHost));
+    if (st & 1) return fail(CWLB_INVALID_ARG, "spmm: a column index is outside [0, h_rows)");
+    if (st & 2) return fail(CWLB_INVALID_ARG, "spmm: an origin entry is outside [0, n_rows)");
+    return CWLB_OK;
+}
+
+cwlb_status run_spmm(cwlb_ctx* ctx, const SpmmArgs& a, uint32_t flags, cwlb_timing* timing)
+{
+    cwlb_status st = check_spmm_args(ctx, a);
+    if (st != CWLB_OK) return st;
+    DeviceGuard g(ctx->device);
+    const bool zero_all = (flags & CWLB_SPMM_ZERO_OUTPUT) != 0;
+    if (a.K == 0 || a.n_tasks == 0) {
+        // The reference returns a zero matrix and time 0 (parallelMatrix.cpp:80-83, 101-104).
+        if (zero_all && a.n_rows > 0 && a.K > 0) {
+            st = launch_spmm_mean(ctx, a, true, false);
+            if (st != CWLB_OK) return st;
+        }
+        if (timing) {
+            CWLB_HIP_TRY(hipStreamSynchronize(ctx->stream));
+            *timing = cwlb_timing{0.0f, 0.0f, 0.0f};
+        }
+        return CWLB_OK;
+    }
+    st = launch_spmm_mean(ctx, a, zero_all, timing != nullptr);
+    if (st != CWLB_OK) return st;
+    if (timing) return finish_timed(ctx, timing);
+    return CWLB_OK;
+}
+
+template <class T>
+struct DevBuf {
+    T* p = nullptr;
+    ~DevBuf()
+    {
+        if (p) (void)hipFree(p);
+    }
+    hipError_t alloc(size_t n) { return hipMalloc(reinterpret_cast<void**>(&p), sizeof(T) * (n ? n : 1)); }
+};
+
+}  // namespace
+}  // namespace cwlb
+
+using namespace cwlb;
+
+extern "C" {
+
+const char* cwlb_version(void) { return CWLB_VERSION_STRING " (gfx950)"; }
+
+const char* cwlb_last_error(void) { return g_last_error.c_str(); }
+
+cwlb_status cwlb_ctx_create(int device, void* stream, cwlb_ctx** out)
+{
+    if (!out) return fail(CWLB_INVALID_ARG, "cwlb_ctx_create: null out");
+    *out = nullptr;
+    int count = 0;
+    CWLB_HIP_TRY(hipGetDeviceCount(&count));
+    if (device < 0 || device >= count) return fail(CWLB_INVALID_ARG, "cwlb_ctx_create: bad device id");
+    DeviceGuard g(device);
+    hipDeviceProp_t prop;
+    CWLB_HIP_TRY(hipGetDeviceProperties(&prop, device));
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail(CWLB_UNSUPPORTED, std::string("cwlb: built for gfx950 only, device is ") +
+                                          prop.gcnArchName);
+    auto* c = new (std::nothrow) cwlb_ctx();
+    if (!c) return fail(CWLB_OOM, "cwlb_ctx_create: out of memory");
+    c->device = device;
+    c->stream = static_cast<hipStream_t>(stream);
+    c->compute_units = prop.multiProcessorCount;
+    c->max_wg = prop.maxThreadsPerBlock;
+    c->wave = prop.warpSize;
+    c->lds_per_block = prop.sharedMemPerBlock;
+    c->total_mem = prop.totalGlobalMem;
+    std::snprintf(c->name, sizeof c->name, "%s", prop.name);
+    std::snprintf(c->arch, sizeof c->arch, "%s", prop.gcnArchName);
+    hipError_t e = hipSuccess;
+    for (auto& ev : c->ev)
+        if (e == hipSuccess) e = hipEventCreate(&ev);
+    if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&c->d_status), sizeof(int));
+    if (e == hipSuccess) e = hipMemset(c->d_status, 0, sizeof(int));
+    if (e != hipSuccess) {
+        cwlb_ctx_destroy(c);
+        return hip_fail(e, "cwlb_ctx_create");
+    }
+    *out = c;
+    return CWLB_OK;
+}
+
+cwlb_status cwlb_ctx_destroy(cwlb_ctx* ctx)
+{
+    if (!ctx) return CWLB_OK;
+    DeviceGuard g(ctx->device);
+    for (auto& ev : ctx->ev)
+        if (ev) (void)hipEventDestroy(ev);
+    if (ctx->d_status) (void)hipFree(ctx->d_status);
+    delete ctx;
+    return CWLB_OK;
+}
+
+cwlb_status cwlb_ctx_set_stream(cwlb_ctx* ctx, void* stream)
+{
+    if (!ctx) return fail(CWLB_INVALID_ARG, "null context");
+    ctx->stream = static_cast<hipStream_t>(stream);
+    return CWLB_OK;
+}
+
+cwlb_status cwlb_ctx_synchronize(cwlb_ctx* ctx)
+{
+    if (!ctx) return fail(CWLB_INVALID_ARG, "null context");
+    DeviceGuard g(ctx->device);
+    CWLB_HIP_TRY(hipStreamSynchronize(ctx->stream));
+    return CWLB_OK;
+}
+
+cwlb_status cwlb_ctx_device_info(cwlb_ctx* ctx, cwlb_device_info* out)
+{
+    if (!ctx || !out) return fail(CWLB_INVALID_ARG, "null argument");
+    out->device = ctx->device;
+    out->compute_units = ctx->compute_units;
+    out->max_work_group_size = ctx->max_wg;
+    out->wavefront_size = ctx->wave;
+    out->lds_bytes_per_block = static_cast<int64_t>(ctx->lds_per_block);
+    out->total_global_mem = static_cast<int64_t>(ctx->total_mem);
+    std::snprintf(out->name, sizeof out->name, "%s", ctx->name);
+    std::snprintf(out->arch, sizeof out->arch, "%s", ctx->arch);
+    return CWLB_OK;
+}
+
+cwlb_status cwlb_spmm_mean_f32(cwlb_ctx* ctx, const int32_t* row_ptr, const int32_t* col_idx,
+                               const float* val, const int32_t* origin, int32_t n_rows,
+                               int64_t nnz, const float* H, int64_t h_rows, int32_t K,
+                               const cwlb_task* tasks, int64_t n_tasks, float* C,
+                               uint32_t flags, cwlb_timing* timing)
+{
+    if (ctx && K > ctx->max_wg)
+        return fail(CWLB_INVALID_ARG,
+                    "spmmKernel supports only K <= device max work-group size; "
+                    "use spmmKernelLargeKFallback for larger K.");
+    SpmmArgs a{row_ptr, col_idx, val, origin, n_rows, nnz, H, h_rows, K, tasks, n_tasks, C};
+    return run_spmm(ctx, a, flags, timing);
+}
+
+cwlb_status cwlb_spmm_mean_f32_large_k(cwlb_ctx* ctx, const int32_t* row_ptr,
+                                       const int32_t* col_idx, const float* val,
+                                       const int32_t* origin, int32_t n_rows, int64_t nnz,
+                                       const float* H, int64_t h_rows, int32_t K,
+                                       const cwlb_task* tasks, int64_t n_tasks, float* C,
+                                       uint32_t flags, cwlb_timing* timing)
+{
+    if (!ctx) return fail(CWLB_INVALID_ARG, "null context");
+    if (ctx->max_wg <= 0)
+        return fail(CWLB_RUNTIME_ERROR,
+                    "Large-K fallback cannot use a device with max_work_group_size=0.");
+    if (K <= ctx->max_wg)
+        return fail(CWLB_INVALID_ARG,
+                    "spmmKernelLargeKFallback requires K > device max work-group size.");
+    SpmmArgs a{row_ptr, col_idx, val, origin, n_rows, nnz, H, h_rows, K, tasks, n_tasks, C};
+    return run_spmm(ctx, a, flags, timing);
+}
+
+cwlb_status cwlb_spmm_mean_f32_host(cwlb_ctx* ctx, const int32_t* row_ptr,
+                                    const int32_t* col_idx, const float* val,
+                                    const int32_t* origin, int32_t n_rows, int64_t nnz,
+                                    const float* H, int64_t h_rows, int32_t K,
+                                    const cwlb_task* tasks, int64_t n_tasks, float* C,
+                                    cwlb_timing* timing)
+{
+    if (!ctx) return fail(CWLB_INVALID_ARG, "null context");
+    if (n_rows < 0 || nnz < 0 || K < 0 || n_tasks < 0 || h_rows < 0)
+        return fail(CWLB_INVALID_ARG, "spmm: negative size");
+    if (nnz > INT32_MAX) return fail(CWLB_INVALID_ARG, "spmm: nnz must fit int32");
+    DeviceGuard g(ctx->device);
+    const size_t out_elems = static_cast<size_t>(n_rows) * static_cast<size_t>(K);
+    if (K == 0 || n_tasks == 0) {
+        if (out_elems) std::memset(C, 0, out_elems * sizeof(float));
+        if (timing) *timing = cwlb_timing{0.0f, 0.0f, 0.0f};
+        return CWLB_OK;
+    }
+    if (!row_ptr || !origin || !tasks || !C || (nnz > 0 && (!col_idx || !val || !H)))
+        return fail(CWLB_INVALID_ARG, "spmm: null host pointer");
+    // Host-side validation keeps every device access in bounds.
+    if (row_ptr[0] < 0 || row_ptr[n_rows] > nnz)
+        return fail(CWLB_INVALID_ARG, "spmm: row_ptr outside [0, nnz]");
+    for (int32_t r = 0; r < n_rows; ++r)
+        if (row_ptr[r + 1] < row_ptr[r])
+            return fail(CWLB_INVALID_ARG, "spmm: row_ptr is not non-decreasing");
+    for (int64_t j = 0; j < nnz; ++j)
+        if (col_idx[j] < 0 || col_idx[j] >= h_rows)
+            return fail(CWLB_INVALID_ARG, "spmm: column index outside [0, h_rows)");
+    DevBuf<int32_t> d_rp, d_ci, d_or;
+    DevBuf<float> d_val, d_H, d_C;
+    DevBuf<cwlb_task> d_t;
+    CWLB_HIP_TRY(d_rp.alloc(static_cast<size_t>(n_rows) + 1));
+    CWLB_HIP_TRY(d_ci.alloc(static_cast<size_t>(nnz)));
+    CWLB_HIP_TRY(d_val.alloc(static_cast<size_t>(nnz)));
+    CWLB_HIP_TRY(d_or.alloc(static_cast<size_t>(n_rows)));
+    CWLB_HIP_TRY(d_H.alloc(static_cast<size_t>(h_rows) * K));
+    CWLB_HIP_TRY(d_C.alloc(out_elems));
+    CWLB_HIP_TRY(d_t.alloc(static_cast<size_t>(n_tasks)));
+    hipStream_t st = ctx->stream;
+    CWLB_HIP_TRY(hipMemcpyAsync(d_rp.p, row_ptr, sizeof(int32_t) * (n_rows + 1), hipMemcpyHostToDevice, st));
+    if (nnz) {
+        CWLB_HIP_TRY(hipMemcpyAsync(d_ci.p, col_idx, sizeof(int32_t) * nnz, hipMemcpyHostToDevice, st));
+        CWLB_HIP_TRY(hipMemcpyAsync(d_val.p, val, sizeof(float) * nnz, hipMemcpyHostToDevice, st));
+    }
+    if (n_rows)
+        CWLB_HIP_TRY(hipMemcpyAsync(d_or.p, origin, sizeof(int32_t) * n_rows, hipMemcpyHostToDevice, st));
+    if (h_rows * K)
+        CWLB_HIP_TRY(hipMemcpyAsync(d_H.p, H, sizeof(float) * h_rows * K, hipMemcpyHostToDevice, st));
+    CWLB_HIP_TRY(hipMemcpyAsync(d_t.p, tasks, sizeof(cwlb_task) * n_tasks, hipMemcpyHostToDevice, st));
+    SpmmArgs a{d_rp.p, d_ci.p, d_val.p, d_or.p, n_rows, nnz, d_H.p, h_rows, K, d_t.p, n_tasks, d_C.p};
+    cwlb_timing local{};
+    cwlb_status s = run_spmm(ctx, a, CWLB_SPMM_ZERO_OUTPUT, &local);
+    if (s != CWLB_OK) return s;
+    if (out_elems)
+        CWLB_HIP_TRY(hipMemcpyAsync(C, d_C.p, sizeof(float) * out_elems, hipMemcpyDeviceToHost, st));
+    CWLB_HIP_TRY(hipStreamSynchronize(st));
+    // The reference times the aggregation kernel only; C's clearing is the
+    // host-side Zero() there.
+    if (timing) *timing = cwlb_timing{0.0f, local.main_us, local.main_us};
+    return CWLB_OK;
+}
+
+cwlb_status cwlb_reorder_by_degree_device(cwlb_ctx* ctx, int32_t n_rows, int64_t nnz,
+                                          const int32_t* row_ptr, const int32_t* col_idx,
+                                          const float* val, int32_t* origin,
+                                          int32_t* row_ptr_out, int32_t* col_idx_out,
+                                          float* val_out)
+{
+    if (!ctx) return fail(CWLB_INVALID_ARG, "null context");
+    if (n_rows < 0 || nnz < 0 || nnz > INT32_MAX)
+        return fail(CWLB_INVALID_ARG, "reorder: bad sizes");
+    DeviceGuard g(ctx->device);
+    return launch_reorder(ctx, n_rows, nnz, row_ptr, col_idx, val, origin, row_ptr_out,
+                          col_idx_out, val_out);
+}
+
+cwlb_status cwlb_calibrate(cwlb_ctx* ctx, int32_t K, int32_t repeat, int32_t WI, int32_t load_MB,
+                           int32_t atomic_writers, cwlb_cost_params* out)
+{
+    if (!ctx || !out) return fail(CWLB_INVALID_ARG, "null argument");
+    if (K <= 0 || repeat <= 0 || WI <= 0 || load_MB <= 0 || atomic_writers <= 0)
+        return fail(CWLB_INVALID_ARG, "All microbenchmark parameters must be positive.");
+    DeviceGuard g(ctx->device);
+    return run_calibration(ctx, K, repeat, WI, load_MB, atomic_writers, out);
+}
+
+cwlb_status cwlb_fill_features_uniform(cwlb_ctx* ctx, float* H, int64_t rows, int32_t K,
+                                       uint64_t seed)
+{
+    if (!ctx) return fail(CWLB_INVALID_ARG, "null context");
+    if (rows < 0 || K < 0) return fail(CWLB_INVALID_ARG, "negative size");
+    if (rows * K > 0 && !H) return fail(CWLB_INVALID_ARG, "null H");
+    DeviceGuard g(ctx->device);
+    return launch_fill_features(ctx, H, rows, K, seed);
+}
+
+}  // extern "C"

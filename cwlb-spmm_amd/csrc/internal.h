@@ -1,0 +1,82 @@
+// Internal declarations shared by the libcwlb translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <string>
+
+#include "cwlb.h"
+
+struct cwlb_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
+    int compute_units = 0;
+    int max_wg = 0;
+    int wave = 64;
+    size_t lds_per_block = 0;
+    size_t total_mem = 0;
+    char name[256] = {0};
+    char arch[64] = {0};
+    // Device status word written by the kernels: bit 0 = a column index was
+    // outside [0, h_rows), bit 1 = an origin entry was outside [0, n_rows).
+    int* d_status = nullptr;
+};
+
+namespace cwlb {
+
+// Thread-local last-error message.
+void set_error(const std::string& msg);
+cwlb_status fail(cwlb_status st, const std::string& msg);
+cwlb_status hip_fail(hipError_t e, const char* what);
+
+#define CWLB_HIP_TRY(expr)                                   \
+    do {                                                     \
+        hipError_t e_ = (expr);                              \
+        if (e_ != hipSuccess) return ::cwlb::hip_fail(e_, #expr); \
+    } while (0)
+
+// Scoped device switch.
+struct DeviceGuard {
+    int prev = -1;
+    explicit DeviceGuard(int dev)
+    {
+        if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+        if (prev != dev) (void)hipSetDevice(dev);
+    }
+    ~DeviceGuard()
+    {
+        if (prev >= 0) (void)hipSetDevice(prev);
+    }
+};
+
+struct SpmmArgs {
+    const int32_t* row_ptr;
+    const int32_t* col_idx;
+    const float* val;
+    const int32_t* origin;
+    int32_t n_rows;
+    int64_t nnz;
+    const float* H;
+    int64_t h_rows;
+    int32_t K;
+    const cwlb_task* tasks;
+    int64_t n_tasks;
+    float* C;
+};
+
+// Enqueues the split-row clearing pass (or the full clear when zero_all)
+// and the aggregation kernel on ctx->stream, bracketed by ctx->ev[0..2].
+cwlb_status launch_spmm_mean(cwlb_ctx* ctx, const SpmmArgs& a, bool zero_all, bool record_events);
+
+cwlb_status launch_fill_features(cwlb_ctx* ctx, float* H, int64_t rows, int32_t K, uint64_t seed);
+
+cwlb_status launch_reorder(cwlb_ctx* ctx, int32_t n_rows, int64_t nnz, const int32_t* row_ptr,
+                           const int32_t* col_idx, const float* val, int32_t* origin,
+                           int32_t* row_ptr_out, int32_t* col_idx_out, float* val_out);
+
+cwlb_status run_calibration(cwlb_ctx* ctx, int32_t K, int32_t repeat, int32_t WI, int32_t load_MB,
+                            int32_t atomic_writers, cwlb_cost_params* out);
+
+}  // namespace cwlb

@@ -1,0 +1,618 @@
+// FP32 mean-aggregation SpMM over a cost-weighted task list, for gfx950.
+//
+// Semantics follow spmmKernel (reference src/parallelMatrix.cpp:148-236):
+// every task is a half-open range of reordered rows whose first row starts
+// at first_row_offset and whose last row ends at last_row_nnz (0 = full
+// degree); for each row chunk the kernel forms
+//     acc[k] = sum_j val[j] * H[col[j]][k]   (fma, CSR order per lane)
+// divides by the FULL degree, then stores C[origin[r]] for a full row or
+// adds atomically for a partial one.  Rows of degree 0 are written as zeros
+// (the reference leaves its host-zeroed C untouched there).
+//
+// Mapping to CDNA4 (64-lane waves):
+//   * one wave executes one task; a block holds kWaves waves (kWaves tasks);
+//   * a row of K floats is covered by a "slot" of G lanes, each lane holding
+//     R vectors of VEC floats (128-bit loads when K % 4 == 0); a wave has
+//     NS = 64 / G slots;
+//   * short rows run row-per-slot, RU rows per slot at a time, each row
+//     summed sequentially in CSR order (bit-identical to the reference's
+//     per-work-item loop);
+//   * a long chunk runs on all slots at once, UL nonzeros in flight per
+//     slot, followed by a shuffle reduction across slots;
+//   * column indices and values are fetched 64 at a time with one coalesced
+//     load and handed to the slots with cross-lane shuffles.
+// Split rows are cleared by zero_first_segments before the main kernel, in
+// the task that owns their first segment, so each is cleared exactly once.
+#include "internal.h"
+
+#include <algorithm>
+
+namespace cwlb {
+namespace {
+
+constexpr int kWaves = 4;
+constexpr int kBlock = 64 * kWaves;
+
+typedef float f2 __attribute__((ext_vector_type(2)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+template <int VEC>
+struct VecT;
+template <>
+struct VecT<1> {
+    using T = float;
+};
+template <>
+struct VecT<2> {
+    using T = f2;
+};
+template <>
+struct VecT<4> {
+    using T = f4;
+};
+
+
+template <int VEC>
+__device__ __forceinline__ typename VecT<VEC>::T vzero()
+{
+    return typename VecT<VEC>::T(0.0f);
+}
+
+template <int VEC>
+__device__ __forceinline__ typename VecT<VEC>::T vload(const float* p)
+{
+    return *reinterpret_cast<const typename VecT<VEC>::T*>(p);
+}
+
+template <int VEC>
+__device__ __forceinline__ void vstore(float* p, typename VecT<VEC>::T v)
+{
+    *reinterpret_cast<typename VecT<VEC>::T*>(p) = v;
+}
+
+__device__ __forceinline__ float vfma(float a, float h, float c) { return __builtin_fmaf(a, h, c); }
+__device__ __forceinline__ f2 vfma(float a, f2 h, f2 c)
+{
+    f2 r;
+    r.x = __builtin_fmaf(a, h.x, c.x);
+    r.y = __builtin_fmaf(a, h.y, c.y);
+    return r;
+}
+__device__ __forceinline__ f4 vfma(float a, f4 h, f4 c)
+{
+    f4 r;
+    r.x = __builtin_fmaf(a, h.x, c.x);
+    r.y = __builtin_fmaf(a, h.y, c.y);
+    r.z = __builtin_fmaf(a, h.z, c.z);
+    r.w = __builtin_fmaf(a, h.w, c.w);
+    return r;
+}
+
+__device__ __forceinline__ float vdiv(float v, float d) { return v / d; }
+__device__ __forceinline__ f2 vdiv(f2 v, float d)
+{
+    f2 r;
+    r.x = v.x / d;
+    r.y = v.y / d;
+    return r;
+}
+__device__ __forceinline__ f4 vdiv(f4 v, float d)
+{
+    f4 r;
+    r.x = v.x / d;
+    r.y = v.y / d;
+    r.z = v.z / d;
+    r.w = v.w / d;
+    return r;
+}
+
+__device__ __forceinline__ float vshfl_xor(float v, int m) { return __shfl_xor(v, m); }
+__device__ __forceinline__ f2 vshfl_xor(f2 v, int m)
+{
+    f2 r;
+    r.x = __shfl_xor(v.x, m);
+    r.y = __shfl_xor(v.y, m);
+    return r;
+}
+__device__ __forceinline__ f4 vshfl_xor(f4 v, int m)
+{
+    f4 r;
+    r.x = __shfl_xor(v.x, m);
+    r.y = __shfl_xor(v.y, m);
+    r.z = __shfl_xor(v.z, m);
+    r.w = __shfl_xor(v.w, m);
+    return r;
+}
+
+__device__ __forceinline__ void vatomic_add(float* p, float v) { unsafeAtomicAdd(p, v); }
+__device__ __forceinline__ void vatomic_add(float* p, f2 v)
+{
+    unsafeAtomicAdd(p, v.x);
+    unsafeAtomicAdd(p + 1, v.y);
+}
+__device__ __forceinline__ void vatomic_add(float* p, f4 v)
+{
+    unsafeAtomicAdd(p, v.x);
+    unsafeAtomicAdd(p + 1, v.y);
+    unsafeAtomicAdd(p + 2, v.z);
+    unsafeAtomicAdd(p + 3, v.w);
+}
+
+__device__ __forceinline__ int wave_max(int v)
+{
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = max(v, __shfl_xor(v, off));
+    return v;
+}
+
+// Nonzero range of row r inside task (rs, re, fo, ln), with the reference's
+// clamps (parallelMatrix.cpp:164-176).  Rows with deg <= 0 have an empty
+// chunk.  A row whose offsets leave [0, nnz) gets an empty chunk too, so no
+// load can leave the arrays.
+struct Chunk {
+    int base;  // row_ptr[r]
+    int b;     // chunk begin within the row
+    int e;     // chunk end within the row
+    int d;     // full degree
+};
+
+__device__ __forceinline__ Chunk row_chunk(const int* __restrict__ rp, int r, int rs, int re,
+                                           int fo, int ln, long long nnz)
+{
+    Chunk c;
+    const int p0 = rp[r];
+    const int p1 = rp[r + 1];
+    c.base = p0;
+    c.d = p1 - p0;
+    c.b = 0;
+    c.e = 0;
+    if (c.d <= 0 || p0 < 0 || static_cast<long long>(p1) > nnz) return c;
+    int b = (r == rs) ? fo : 0;
+    int e = c.d;
+    if (r == re - 1 && ln > 0) e = ln;
+    b = min(max(b, 0), c.d);
+    e = min(max(e, b), c.d);
+    c.b = b;
+    c.e = e;
+    return c;
+}
+
+constexpr int cmin(int a, int b) { return a < b ? a : b; }
+
+template <int VEC, int G, int R, int U>
+__global__ void __launch_bounds__(kBlock)
+spmm_mean_tasks(const int* __restrict__ rp, const int* __restrict__ ci,
+                const float* __restrict__ val, const int* __restrict__ origin, int n_rows,
+                long long nnz, const float* __restrict__ H, long long h_rows, int K,
+                const cwlb_task* __restrict__ tasks, long long n_tasks, float* __restrict__ C,
+                int* __restrict__ status)
+{
+    using V = typename VecT<VEC>::T;
+    constexpr int NS = 64 / G;                     // row slots per wave
+    constexpr int RU = cmin(cmin(U, 4), G);        // rows per slot (short rows)
+    constexpr int GROUP = NS * RU;                 // rows per short-row group (<= 64)
+    constexpr int UL = cmin(U, G);                 // nonzeros per slot per step (long rows)
+    constexpr int STEP = NS * UL;                  // nonzeros per wave step (<= 64)
+    constexpr int kLong = GROUP > 2 ? GROUP : 2;   // chunk length that runs on all slots
+
+    const int lane = threadIdx.x & 63;
+    const int slot = lane / G;
+    const int sub = lane - slot * G;
+    const long long t = static_cast<long long>(blockIdx.x) * kWaves +
+                        __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if (t >= n_tasks) return;
+
+    const cwlb_task tk = tasks[t];
+    const int rs = tk.row_start;
+    const int re = tk.row_end;
+    const int fo = tk.first_row_offset;
+    const int ln = tk.last_row_nnz;
+    const int rlo = max(rs, 0);
+    const int rhi = min(re, n_rows);
+    const int F = K / VEC;
+    const int npass = (F + G * R - 1) / (G * R);
+    int bad = 0;
+
+    for (int pass = 0; pass < npass; ++pass) {
+        const int fl = pass * G * R + sub;  // first vector element of this lane
+        int r = rlo;
+        while (r < rhi) {
+            const Chunk c0 = row_chunk(rp, r, rs, re, fo, ln, nnz);
+            const int len0 = c0.e - c0.b;
+            if (len0 >= kLong) {
+                // ---------------- long chunk: all slots on one row
+                V acc[R];
+#pragma unroll
+                for (int q = 0; q < R; ++q) acc[q] = vzero<VEC>();
+                for (int w0 = c0.b; w0 < c0.e; w0 += 64) {
+                    const int wn = min(64, c0.e - w0);
+                    int colw = 0;
+                    float valw = 0.0f;
+                    if (lane < wn) {
+                        colw = ci[c0.base + w0 + lane];
+                        valw = val[c0.base + w0 + lane];
+                    }
+                    for (int k0 = 0; k0 < wn; k0 += STEP) {
+                        int cc[UL];
+                        float a[UL];
+                        bool ok[UL];
+#pragma unroll
+                        for (int u = 0; u < UL; ++u) {
+                            const int jj = k0 + u * NS + slot;
+                            cc[u] = __shfl(colw, jj & 63);
+                            a[u] = __shfl(valw, jj & 63);
+                            ok[u] = jj < wn;
+                            if (ok[u] && static_cast<unsigned long long>(cc[u]) >=
+                                             static_cast<unsigned long long>(h_rows)) {
+                                ok[u] = false;
+                                bad |= 1;
+                            }
+                        }
+                        V h[UL][R];
+#pragma unroll
+                        for (int u = 0; u < UL; ++u) {
+                            const float* hrow = H + static_cast<size_t>(cc[u]) * K;
+#pragma unroll
+                            for (int q = 0; q < R; ++q) {
+                                const int f = fl + G * q;
+                                h[u][q] = (ok[u] && f < F) ? vload<VEC>(hrow + f * VEC)
+                                                           : vzero<VEC>();
+                            }
+                        }
+#pragma unroll
+                        for (int u = 0; u < UL; ++u) {
+                            if (ok[u]) {
+#pragma unroll
+                                for (int q = 0; q < R; ++q) acc[q] = vfma(a[u], h[u][q], acc[q]);
+                            }
+                        }
+                    }
+                }
+#pragma unroll
+                for (int off = G; off < 64; off <<= 1) {
+#pragma unroll
+                    for (int q = 0; q < R; ++q) acc[q] = acc[q] + vshfl_xor(acc[q], off);
+                }
+                const int o = origin[r];
+                if (static_cast<unsigned>(o) >= static_cast<unsigned>(n_rows)) {
+                    bad |= 2;
+                } else if (slot == 0) {
+                    float* crow = C + static_cast<size_t>(o) * K;
+                    const float fd = static_cast<float>(c0.d);
+                    const bool full = (c0.b == 0 && c0.e == c0.d);
+#pragma unroll
+                    for (int q = 0; q < R; ++q) {
+                        const int f = fl + G * q;
+                        if (f < F) {
+                            const V res = vdiv(acc[q], fd);
+                            if (full)
+                                vstore<VEC>(crow + f * VEC, res);
+                            else
+                                vatomic_add(crow + f * VEC, res);
+                        }
+                    }
+                }
+                ++r;
+                continue;
+            }
+
+            // ---------------- short rows: one row per slot, RU rows per slot
+            const int rr = r + lane;
+            const bool mine = lane < GROUP && rr < rhi;
+            Chunk my = {0, 0, 0, 0};
+            if (mine) my = row_chunk(rp, rr, rs, re, fo, ln, nnz);
+            const int mylen = my.e - my.b;
+            const unsigned long long lm = __ballot(mine && mylen >= kLong);
+            int cnt = min(GROUP, rhi - r);
+            if (lm) cnt = min(cnt, static_cast<int>(__ffsll(static_cast<long long>(lm))) - 1);
+            const int myo = (mine && lane < cnt) ? origin[rr] : 0;
+            // Nonzeros of the group are contiguous: [gs, ge).
+            const int gs = c0.base + c0.b;
+            const int ge = __shfl(my.base + my.e, cnt - 1);
+            const bool win = (ge - gs) <= 64 && ge >= gs;
+            int colw = 0;
+            float valw = 0.0f;
+            if (win && lane < ge - gs && gs >= 0 && static_cast<long long>(gs) + lane < nnz) {
+                colw = ci[gs + lane];
+                valw = val[gs + lane];
+            }
+            V acc[RU][R];
+            int pos[RU];
+            int len[RU];
+            int maxlen = 0;
+#pragma unroll
+            for (int u = 0; u < RU; ++u) {
+                const int gi = u * NS + slot;
+                pos[u] = __shfl(my.base + my.b, gi);
+                len[u] = __shfl(mylen, gi);
+                if (gi >= cnt) len[u] = 0;
+                maxlen = max(maxlen, len[u]);
+#pragma unroll
+                for (int q = 0; q < R; ++q) acc[u][q] = vzero<VEC>();
+            }
+            const int jmax = wave_max(maxlen);
+            for (int j = 0; j < jmax; ++j) {
+                int cc[RU];
+                float a[RU];
+                bool ok[RU];
+#pragma unroll
+                for (int u = 0; u < RU; ++u) {
+                    const int gp = pos[u] + j;
+                    ok[u] = j < len[u];
+                    if (win) {
+                        const int src = (gp - gs) & 63;
+                        cc[u] = __shfl(colw, src);
+                        a[u] = __shfl(valw, src);
+                    } else {
+                        cc[u] = ok[u] ? ci[gp] : 0;
+                        a[u] = ok[u] ? val[gp] : 0.0f;
+                    }
+                    if (ok[u] && static_cast<unsigned long long>(cc[u]) >=
+                                     static_cast<unsigned long long>(h_rows)) {
+                        ok[u] = false;
+                        bad |= 1;
+                    }
+                }
+                V h[RU][R];
+#pragma unroll
+                for (int u = 0; u < RU; ++u) {
+                    const float* hrow = H + static_cast<size_t>(cc[u]) * K;
+#pragma unroll
+                    for (int q = 0; q < R; ++q) {
+                        const int f = fl + G * q;
+                        h[u][q] = (ok[u] && f < F) ? vload<VEC>(hrow + f * VEC) : vzero<VEC>();
+                    }
+                }
+#pragma unroll
+                for (int u = 0; u < RU; ++u) {
+                    if (ok[u]) {
+#pragma unroll
+                        for (int q = 0; q < R; ++q) acc[u][q] = vfma(a[u], h[u][q], acc[u][q]);
+                    }
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < RU; ++u) {
+                const int gi = u * NS + slot;
+                const int o = __shfl(myo, gi);
+                const int d = __shfl(my.d, gi);
+                const int b = __shfl(my.b, gi);
+                const int e = __shfl(my.e, gi);
+                if (gi < cnt) {
+                    if (static_cast<unsigned>(o) >= static_cast<unsigned>(n_rows)) {
+                        bad |= 2;
+                        continue;
+                    }
+                    float* crow = C + static_cast<size_t>(o) * K;
+                    if (d <= 0) {
+#pragma unroll
+                        for (int q = 0; q < R; ++q) {
+                            const int f = fl + G * q;
+                            if (f < F) vstore<VEC>(crow + f * VEC, vzero<VEC>());
+                        }
+                    } else if (e > b) {
+                        const float fd = static_cast<float>(d);
+                        const bool full = (b == 0 && e == d);
+#pragma unroll
+                        for (int q = 0; q < R; ++q) {
+                            const int f = fl + G * q;
+                            if (f < F) {
+                                const V res = vdiv(acc[u][q], fd);
+                                if (full)
+                                    vstore<VEC>(crow + f * VEC, res);
+                                else
+                                    vatomic_add(crow + f * VEC, res);
+                            }
+                        }
+                    }
+                }
+            }
+            r += cnt;
+        }
+    }
+    if (bad) atomicOr(status, bad);
+}
+
+// Clears, once each, the C rows that receive atomic partial sums: a row is
+// cleared by the task whose chunk of it starts at nonzero 0 without reaching
+// the row's end.  One lane per task; the wave then clears the marked rows
+// with coalesced stores.  Block 0 also resets the status word.
+template <int VEC>
+__global__ void __launch_bounds__(kBlock)
+zero_first_segments(const int* __restrict__ rp, const int* __restrict__ origin, int n_rows,
+                    long long nnz, const cwlb_task* __restrict__ tasks, long long n_tasks,
+                    int K, float* __restrict__ C, int* __restrict__ status)
+{
+    const int lane = threadIdx.x & 63;
+    const long long t = static_cast<long long>(blockIdx.x) * kBlock + threadIdx.x;
+    if (blockIdx.x == 0 && threadIdx.x == 0) *status = 0;
+    int o1 = -1, o2 = -1;
+    if (t < n_tasks) {
+        const cwlb_task tk = tasks[t];
+        const int rlo = max(tk.row_start, 0);
+        const int rhi = min(tk.row_end, n_rows);
+        if (rlo < rhi) {
+            const Chunk a = row_chunk(rp, rlo, tk.row_start, tk.row_end, tk.first_row_offset,
+                                      tk.last_row_nnz, nnz);
+            if (a.d > 0 && a.b == 0 && a.e > 0 && a.e < a.d) o1 = origin[rlo];
+            if (rhi - 1 != rlo) {
+                const Chunk z = row_chunk(rp, rhi - 1, tk.row_start, tk.row_end,
+                                          tk.first_row_offset, tk.last_row_nnz, nnz);
+                if (z.d > 0 && z.b == 0 && z.e > 0 && z.e < z.d) o2 = origin[rhi - 1];
+            }
+        }
+        if (o1 >= n_rows) o1 = -1;
+        if (o2 >= n_rows) o2 = -1;
+    }
+    const int F = K / VEC;
+    unsigned long long m = __ballot(o1 >= 0);
+    while (m) {
+        const int src = __ffsll(static_cast<long long>(m)) - 1;
+        m &= m - 1;
+        const int row = __shfl(o1, src);
+        float* crow = C + static_cast<size_t>(row) * K;
+        for (int f = lane; f < F; f += 64) vstore<VEC>(crow + f * VEC, vzero<VEC>());
+    }
+    m = __ballot(o2 >= 0);
+    while (m) {
+        const int src = __ffsll(static_cast<long long>(m)) - 1;
+        m &= m - 1;
+        const int row = __shfl(o2, src);
+        float* crow = C + static_cast<size_t>(row) * K;
+        for (int f = lane; f < F; f += 64) vstore<VEC>(crow + f * VEC, vzero<VEC>());
+    }
+}
+
+// Clears n floats (graph-capture safe, unlike a memset node).
+__global__ void __launch_bounds__(kBlock) fill_zero(float* __restrict__ p, long long n,
+                                                    int* __restrict__ status)
+{
+    if (blockIdx.x == 0 && threadIdx.x == 0 && status) *status = 0;
+    const long long n4 = n / 4;
+    f4* p4 = reinterpret_cast<f4*>(p);
+    const long long stride = static_cast<long long>(gridDim.x) * blockDim.x;
+    for (long long i = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x; i < n4;
+         i += stride)
+        p4[i] = f4(0.0f);
+    for (long long i = n4 * 4 + static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
+         i < n; i += stride)
+        p[i] = 0.0f;
+}
+
+__device__ __forceinline__ unsigned long long mix64(unsigned long long z)
+{
+    z += 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+__global__ void __launch_bounds__(kBlock)
+fill_features(float* __restrict__ H, long long total, unsigned long long s)
+{
+    const long long stride = static_cast<long long>(gridDim.x) * blockDim.x;
+    for (long long i = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
+         i += stride) {
+        const unsigned long long x = mix64(s + static_cast<unsigned long long>(i));
+        const int u = static_cast<int>(x >> 40);
+        H[i] = static_cast<float>(u - 8388608) * 0x1.0p-23f;
+    }
+}
+
+unsigned long long host_mix64(unsigned long long z)
+{
+    z += 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+template <int VEC, int G, int R>
+void launch_main(hipStream_t st, const SpmmArgs& a, int* status)
+{
+    constexpr int U = (R == 1) ? 8 : (R == 2) ? 4 : (R <= 4) ? 2 : 1;
+    const long long blocks = (a.n_tasks + kWaves - 1) / kWaves;
+    hipLaunchKernelGGL((spmm_mean_tasks<VEC, G, R, U>), dim3(static_cast<unsigned>(blocks)),
+                       dim3(kBlock), 0, st, a.row_ptr, a.col_idx, a.val, a.origin, a.n_rows,
+                       static_cast<long long>(a.nnz), a.H, static_cast<long long>(a.h_rows), a.K,
+                       a.tasks, static_cast<long long>(a.n_tasks), a.C, status);
+}
+
+template <int VEC>
+void dispatch_main(hipStream_t st, const SpmmArgs& a, int* status)
+{
+    const int F = a.K / VEC;
+    if (F <= 64) {
+        int G = 1;
+        while (G < F) G <<= 1;
+        switch (G) {
+        case 1: return launch_main<VEC, 1, 1>(st, a, status);
+        case 2: return launch_main<VEC, 2, 1>(st, a, status);
+        case 4: return launch_main<VEC, 4, 1>(st, a, status);
+        case 8: return launch_main<VEC, 8, 1>(st, a, status);
+        case 16: return launch_main<VEC, 16, 1>(st, a, status);
+        case 32: return launch_main<VEC, 32, 1>(st, a, status);
+        default: return launch_main<VEC, 64, 1>(st, a, status);
+        }
+    }
+    const int R = std::min((F + 63) / 64, 8);
+    switch (R) {
+    case 2: return launch_main<VEC, 64, 2>(st, a, status);
+    case 3: return launch_main<VEC, 64, 3>(st, a, status);
+    case 4: return launch_main<VEC, 64, 4>(st, a, status);
+    case 5: return launch_main<VEC, 64, 5>(st, a, status);
+    case 6: return launch_main<VEC, 64, 6>(st, a, status);
+    case 7: return launch_main<VEC, 64, 7>(st, a, status);
+    default: return launch_main<VEC, 64, 8>(st, a, status);
+    }
+}
+
+template <int VEC>
+void launch_zero(hipStream_t st, const SpmmArgs& a, int* status)
+{
+    const long long blocks = (a.n_tasks + kBlock - 1) / kBlock;
+    hipLaunchKernelGGL(zero_first_segments<VEC>, dim3(static_cast<unsigned>(blocks)),
+                       dim3(kBlock), 0, st, a.row_ptr, a.origin, a.n_rows,
+                       static_cast<long long>(a.nnz), a.tasks,
+                       static_cast<long long>(a.n_tasks), a.K, a.C, status);
+}
+
+int pick_vec(const SpmmArgs& a)
+{
+    const auto h = reinterpret_cast<uintptr_t>(a.H);
+    const auto c = reinterpret_cast<uintptr_t>(a.C);
+    if (a.K % 4 == 0 && h % 16 == 0 && c % 16 == 0) return 4;
+    if (a.K % 2 == 0 && h % 8 == 0 && c % 8 == 0) return 2;
+    return 1;
+}
+
+}  // namespace
+
+cwlb_status launch_spmm_mean(cwlb_ctx* ctx, const SpmmArgs& a, bool zero_all, bool record_events)
+{
+    hipStream_t st = ctx->stream;
+    if (record_events) CWLB_HIP_TRY(hipEventRecord(ctx->ev[0], st));
+    const long long total = static_cast<long long>(a.n_rows) * a.K;
+    if (zero_all) {
+        if (total > 0) {
+            const long long want = (total / 4 + kBlock - 1) / kBlock;
+            const unsigned blocks = static_cast<unsigned>(std::max<long long>(1, std::min<long long>(want, 65536)));
+            hipLaunchKernelGGL(fill_zero, dim3(blocks), dim3(kBlock), 0, st, a.C, total,
+                               ctx->d_status);
+        } else {
+            hipLaunchKernelGGL(fill_zero, dim3(1), dim3(kBlock), 0, st, a.C, 0LL, ctx->d_status);
+        }
+    }
+    const int vec = pick_vec(a);
+    if (!zero_all && a.n_tasks > 0 && a.K > 0) {
+        if (vec == 4) launch_zero<4>(st, a, ctx->d_status);
+        else if (vec == 2) launch_zero<2>(st, a, ctx->d_status);
+        else launch_zero<1>(st, a, ctx->d_status);
+    } else if (!zero_all) {
+        hipLaunchKernelGGL(fill_zero, dim3(1), dim3(kBlock), 0, st, a.C, 0LL, ctx->d_status);
+    }
+    CWLB_HIP_TRY(hipGetLastError());
+    if (record_events) CWLB_HIP_TRY(hipEventRecord(ctx->ev[1], st));
+    if (a.n_tasks > 0 && a.K > 0) {
+        if (vec == 4) dispatch_main<4>(st, a, ctx->d_status);
+        else if (vec == 2) dispatch_main<2>(st, a, ctx->d_status);
+        else dispatch_main<1>(st, a, ctx->d_status);
+        CWLB_HIP_TRY(hipGetLastError());
+    }
+    if (record_events) CWLB_HIP_TRY(hipEventRecord(ctx->ev[2], st));
+    return CWLB_OK;
+}
+
+cwlb_status launch_fill_features(cwlb_ctx* ctx, float* H, int64_t rows, int32_t K, uint64_t seed)
+{
+    const long long total = static_cast<long long>(rows) * K;
+    if (total <= 0) return CWLB_OK;
+    const unsigned blocks =
+        static_cast<unsigned>(std::min<long long>((total + kBlock - 1) / kBlock, 65536));
+    hipLaunchKernelGGL(fill_features, dim3(blocks), dim3(kBlock), 0, ctx->stream, H, total,
+                       host_mix64(seed));
+    CWLB_HIP_TRY(hipGetLastError());
+    return CWLB_OK;
+}
+
+}  // namespace cwlb

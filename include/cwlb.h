@@ -1,0 +1,234 @@
+/*
+ * cwlb.h -- C ABI of the MI355X (gfx950) CWLB-SpMM library, libcwlb.so.
+ *
+ * FP32 mean-aggregation SpMM over a degree-reordered CSR, executed as the
+ * cost-weighted task list of CWLB-SpMM, plus the host preprocessing around
+ * it (degree reordering, cost-weighted partitioning, segment-size
+ * selection, cost calibration and the cost file).
+ *
+ * Conventions
+ *   - Plain C types only; int32 CSR arrays, float32 values and features,
+ *     row-major dense matrices (row r of H at H + r*K).
+ *   - Every call returns cwlb_status; on failure cwlb_last_error() gives a
+ *     thread-local message.
+ *   - Device-pointer calls are enqueued on the context's HIP stream; they
+ *     synchronise only when a timing struct is requested.
+ *   - A context is used by one host thread at a time.
+ * The C++17 drop-in headers (Matrix.h, utils.h, parallelMatrix.h, ...)
+ * are thin wrappers over these entry points.
+ */
+#ifndef CWLB_H
+#define CWLB_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CWLB_VERSION_STRING "0.1.0"
+
+typedef enum cwlb_status {
+    CWLB_OK = 0,
+    CWLB_INVALID_ARG = 1,     /* std::invalid_argument in the reference */
+    CWLB_UNSUPPORTED = 2,     /* configuration the device cannot run */
+    CWLB_HIP_ERROR = 3,       /* a HIP runtime call failed */
+    CWLB_OOM = 4,             /* host or device allocation failed */
+    CWLB_IO_ERROR = 5,        /* file could not be opened / parsed / written */
+    CWLB_INSUFFICIENT = 6,    /* output buffer too small; size reported */
+    CWLB_RUNTIME_ERROR = 7    /* std::runtime_error in the reference */
+} cwlb_status;
+
+/* One task: half-open range of reordered rows; the first row starts at
+ * first_row_offset nonzeros, the last row ends at last_row_nnz nonzeros
+ * (0 = its full degree).  Same layout as ParallelDataWeighted
+ * (reference include/utils.h:15-20). */
+typedef struct cwlb_task {
+    int32_t row_start;
+    int32_t row_end;
+    int32_t first_row_offset;
+    int32_t last_row_nnz;
+} cwlb_task;
+
+/* Calibrated operation weights (ns per op per work-item, x10) and the
+ * calibration metadata.  Same fields as SpmmCostParams (reference
+ * include/utils.h:23-33). */
+typedef struct cwlb_cost_params {
+    double C_compute_ns;
+    double C_load_ns;
+    double C_store_ns;
+    double C_atomic_ns;
+    int32_t K;
+    int32_t WI;
+    int32_t repeat;
+    int32_t atomic_writers_per_addr;
+} cwlb_cost_params;
+
+/* Kernel timings of one SpMM call, from HIP events on the context stream
+ * (microseconds).  zero_us: clearing the rows that receive atomic partial
+ * sums; main_us: the aggregation kernel; total_us: both. */
+typedef struct cwlb_timing {
+    float zero_us;
+    float main_us;
+    float total_us;
+} cwlb_timing;
+
+typedef struct cwlb_device_info {
+    int32_t device;
+    int32_t compute_units;        /* 256 on MI355X */
+    int32_t max_work_group_size;  /* 1024 */
+    int32_t wavefront_size;       /* 64 */
+    int64_t lds_bytes_per_block;
+    int64_t total_global_mem;
+    char name[256];
+    char arch[64];                /* gcnArchName, e.g. "gfx950:sramecc+:xnack-" */
+} cwlb_device_info;
+
+typedef struct cwlb_ctx cwlb_ctx;
+
+/* ---------------------------------------------------------------- basics */
+const char* cwlb_version(void);
+const char* cwlb_last_error(void);
+
+/* Creates a context on HIP device `device` that launches on `stream`
+ * (a hipStream_t; NULL selects the null stream).  Replaces the
+ * sycl::queue the reference passes around (main.cpp:514-516). */
+cwlb_status cwlb_ctx_create(int device, void* stream, cwlb_ctx** out);
+cwlb_status cwlb_ctx_destroy(cwlb_ctx* ctx);
+cwlb_status cwlb_ctx_set_stream(cwlb_ctx* ctx, void* stream);
+cwlb_status cwlb_ctx_synchronize(cwlb_ctx* ctx);
+cwlb_status cwlb_ctx_device_info(cwlb_ctx* ctx, cwlb_device_info* out);
+
+/* ------------------------------------------------------------ aggregation
+ * C[Origin_local[r]][k] = (sum over the task chunks of row r of
+ *   val[j] * H[col_idx[j]][k]) / deg(r)
+ * executed per task as in spmmKernel (reference parallelMatrix.cpp:63-254):
+ * a chunk that is the full row is stored, a partial chunk is added
+ * atomically (after its row was cleared), rows of degree 0 are written as
+ * zeros.  All pointers are device pointers: row_ptr[n_rows+1],
+ * col_idx[nnz], val[nnz], origin[n_rows], H[h_rows*K], tasks[n_tasks],
+ * C[n_rows*K].
+ *
+ * Preconditions checked on the host: n_rows >= 0, nnz >= 0, K >= 0,
+ * n_tasks >= 0, non-null pointers for non-empty arrays.  Task entries are
+ * validated on the device-side for bounds (row ranges clamped as in the
+ * reference, parallelMatrix.cpp:169-176); column indices must be < h_rows.
+ * With the flag CWLB_SPMM_ZERO_OUTPUT the whole of C is cleared first (the
+ * reference's host-side Zero(), parallelMatrix.cpp:112), which makes any
+ * task list behave as in the reference; without it, rows that no task
+ * touches keep their previous contents (a partition from
+ * cwlb_partition touches every row).
+ * K == 0 or n_tasks == 0: C is cleared (when CWLB_SPMM_ZERO_OUTPUT is set)
+ * and timings are 0, as the reference returns a zero matrix with time 0
+ * (parallelMatrix.cpp:80-83, 101-104).
+ * timing may be NULL (asynchronous); otherwise the call synchronises.
+ *
+ * cwlb_spmm_mean_f32 mirrors spmmKernel: K > max work-group size (1024)
+ * returns CWLB_INVALID_ARG (parallelMatrix.cpp:84-88).
+ * cwlb_spmm_mean_f32_large_k mirrors spmmKernelLargeKFallback: it requires
+ * K > max work-group size (parallelMatrix.cpp:287-290). */
+#define CWLB_SPMM_ZERO_OUTPUT 0x1u
+
+cwlb_status cwlb_spmm_mean_f32(cwlb_ctx* ctx, const int32_t* row_ptr, const int32_t* col_idx,
+                               const float* val, const int32_t* origin, int32_t n_rows,
+                               int64_t nnz, const float* H, int64_t h_rows, int32_t K,
+                               const cwlb_task* tasks, int64_t n_tasks, float* C,
+                               uint32_t flags, cwlb_timing* timing);
+
+cwlb_status cwlb_spmm_mean_f32_large_k(cwlb_ctx* ctx, const int32_t* row_ptr,
+                                       const int32_t* col_idx, const float* val,
+                                       const int32_t* origin, int32_t n_rows, int64_t nnz,
+                                       const float* H, int64_t h_rows, int32_t K,
+                                       const cwlb_task* tasks, int64_t n_tasks, float* C,
+                                       uint32_t flags, cwlb_timing* timing);
+
+/* Host-pointer form: copies the inputs to the device, runs the call, copies
+ * C back (the reference's per-call sycl::buffer behaviour,
+ * parallelMatrix.cpp:115-121).  C is always cleared first.  Dispatches on K
+ * like run_single_s (main.cpp:359-365).  Timing covers the kernels only. */
+cwlb_status cwlb_spmm_mean_f32_host(cwlb_ctx* ctx, const int32_t* row_ptr,
+                                    const int32_t* col_idx, const float* val,
+                                    const int32_t* origin, int32_t n_rows, int64_t nnz,
+                                    const float* H, int64_t h_rows, int32_t K,
+                                    const cwlb_task* tasks, int64_t n_tasks, float* C,
+                                    cwlb_timing* timing);
+
+/* ----------------------------------------------------------- preprocessing
+ * Degree reordering, sortCSRByDegreeDPLCPU (reference main.cpp:197-278):
+ * rows ordered by (degree, original id) ascending; origin[new] = old;
+ * row_ptr_out is the inclusive scan of the sorted degrees; each row's
+ * entries keep their order.  Host arrays.  Returns CWLB_RUNTIME_ERROR when
+ * row_ptr[n_rows] != nnz (the reference's inconsistent-nnz error). */
+cwlb_status cwlb_reorder_by_degree(int32_t n_rows, int64_t nnz, const int32_t* row_ptr,
+                                   const int32_t* col_idx, const float* val, int32_t* origin,
+                                   int32_t* row_ptr_out, int32_t* col_idx_out, float* val_out);
+
+/* The same permutation and arrays computed on the GPU from device arrays
+ * (stable counting sort by degree + row gather).  Bit-identical to
+ * cwlb_reorder_by_degree.  Synchronises. */
+cwlb_status cwlb_reorder_by_degree_device(cwlb_ctx* ctx, int32_t n_rows, int64_t nnz,
+                                          const int32_t* row_ptr, const int32_t* col_idx,
+                                          const float* val, int32_t* origin,
+                                          int32_t* row_ptr_out, int32_t* col_idx_out,
+                                          float* val_out);
+
+/* Cost-weighted task partitioning, costWeightedTaskPartitioning (reference
+ * utils.cpp:832-1021), bit-exact.  row_ptr is the reordered CSR's host
+ * offsets (n_rows + 1 entries; n_rows <= 0 gives no tasks).  Writes at most
+ * capacity_tasks tasks to out (may be NULL when capacity_tasks == 0) and
+ * stores the full count in *n_tasks; returns CWLB_INSUFFICIENT when the
+ * buffer was too small. */
+cwlb_status cwlb_partition(const int32_t* row_ptr, int32_t n_rows, const cwlb_cost_params* costs,
+                           double capacity_weight, cwlb_task* out, int64_t capacity_tasks,
+                           int64_t* n_tasks);
+
+/* --------------------------------------------------- segment-size selection
+ * capacity_from_s (reference main.cpp:281-292). */
+double cwlb_capacity_from_s(int32_t s, const cwlb_cost_params* costs);
+/* wave_based_s (main.cpp:295-321): S = clamp(ceil(nnz/(cu*wave)), 1,
+ * INT_MAX); row_ptr_len == 0 (empty RowOffset) gives 1.  Non-positive cu or
+ * wave -> CWLB_INVALID_ARG. */
+cwlb_status cwlb_wave_based_s(int64_t nnz, int64_t row_ptr_len, int32_t compute_units,
+                              int32_t wave, int32_t* s_out);
+/* recommended_candidate_w (main.cpp:87-95). */
+void cwlb_recommended_candidate_w(uint64_t nnz, int32_t out3[3]);
+/* candidate_search_bounds (main.cpp:109-127). */
+cwlb_status cwlb_candidate_search_bounds(const int32_t values3[3], int64_t best_index,
+                                         int32_t* lower, int32_t* upper);
+/* candidate_search_by_count / _by_step (main.cpp:130-167); two-call sizing
+ * as cwlb_partition. */
+cwlb_status cwlb_candidate_search_by_count(int32_t lower, int32_t upper, int32_t requested,
+                                           int32_t* out, int64_t capacity, int64_t* count);
+cwlb_status cwlb_candidate_search_by_step(int32_t lower, int32_t upper, int32_t step,
+                                          int32_t* out, int64_t capacity, int64_t* count);
+
+/* ------------------------------------------------------------- calibration
+ * measure_spmm_costs (reference utils.cpp:342-829) on gfx950: compute,
+ * load, store and atomic micro-benchmarks, 20 warm-ups and `repeat` timed
+ * launches each, coefficients in ns per op per work-item x10.  The load
+ * benchmark groups lanes by 64 (one wave) instead of the reference's 32.
+ * Fills out->K, WI, repeat and atomic_writers_per_addr too. */
+cwlb_status cwlb_calibrate(cwlb_ctx* ctx, int32_t K, int32_t repeat, int32_t WI,
+                           int32_t load_MB, int32_t atomic_writers, cwlb_cost_params* out);
+
+/* Cost file (utils.cpp:1024-1092): four lines compute/load/store/atomic,
+ * fixed notation with `precision` decimals; the parent directory is
+ * created; a parent that exists as a file fails.  Returns CWLB_IO_ERROR on
+ * failure. */
+cwlb_status cwlb_save_costs(const cwlb_cost_params* costs, const char* path, int append,
+                            int precision);
+cwlb_status cwlb_read_costs(cwlb_cost_params* out, const char* path);
+
+/* -------------------------------------------------------------- utilities
+ * Features in U[-1, 1) written on the device, bit-identical to the host
+ * generator used by the tests: value(i) = (int(top 24 bits of
+ * mix64(mix64(seed) + i)) - 2^23) * 2^-23 for i = row*K + k. */
+cwlb_status cwlb_fill_features_uniform(cwlb_ctx* ctx, float* H, int64_t rows, int32_t K,
+                                       uint64_t seed);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CWLB_H */

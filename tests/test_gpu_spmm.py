@@ -1,0 +1,357 @@
+"""GPU parity of the HIP mean-aggregation SpMM against the oracle.
+
+Every case runs the C ABI (libcwlb.so) on an MI355X and compares with
+  * oracle.spmm_mean_f32: the reference kernel's value order
+    (parallelMatrix.cpp:148-236) on the CPU, and
+  * oracle.spmm_mean_f64: the closed form (A H)[i] / deg(i) on the original
+    CSR, independent of the permutation and the partition.
+Tolerance (from the parity contract): |gpu - ref| <= 1e-6 + 1e-5 * |ref|
+per element.  Full-size configurations are checked through properties that
+do not need the CPU oracle over the whole graph: all-ones features give
+exactly 1 (unit values) or 0 (degree-0 rows), and sampled rows match the
+fp64 closed form.
+"""
+import numpy as np
+import pytest
+
+import oracle
+from conftest import SKEWED_COSTS, UNIT_COSTS
+from cwlb_amd import capi, synth, workloads
+
+pytestmark = pytest.mark.gpu
+
+RTOL, ATOL = 1e-5, 1e-6
+
+
+def torch_mod():
+    import torch
+    return torch
+
+
+def dev(a, dtype=None):
+    torch = torch_mod()
+    a = np.ascontiguousarray(a)
+    if a.size == 0:
+        a = np.zeros(1, a.dtype if dtype is None else dtype)
+    return torch.from_numpy(a).cuda()
+
+
+def run_gpu(ctx, p, H, flags=0, c_fill=float("nan"), large_k=False, h_dev=None):
+    """Runs the device-pointer SpMM on prepared problem p; returns (C, timing)."""
+    torch = torch_mod()
+    K = H.shape[1] if H is not None else h_dev.shape[1]
+    h_rows = H.shape[0] if H is not None else h_dev.shape[0]
+    d_rp, d_ci, d_v, d_o = dev(p.row_ptr), dev(p.col_idx), dev(p.val), dev(p.origin)
+    d_t = dev(np.ascontiguousarray(p.tasks, np.int32).reshape(-1))
+    d_H = dev(H) if h_dev is None else h_dev
+    C = torch.full((max(p.n, 1), max(K, 1)), c_fill, dtype=torch.float32, device="cuda")
+    t = ctx.spmm(d_rp, d_ci, d_v, d_o, p.n, p.nnz, d_H, h_rows, K, d_t, len(p.tasks), C,
+                 flags=flags, large_k=large_k)
+    return C[:p.n, :K].cpu().numpy(), t
+
+
+def check(got, ref):
+    np.testing.assert_allclose(got, ref, rtol=RTOL, atol=ATOL)
+
+
+def problem(g, costs, S):
+    return workloads.prepare(g, costs, S)
+
+
+def oracle_pair(p, g, H):
+    ref32 = oracle.spmm_mean_f32(p.row_ptr, p.col_idx, p.val, p.origin, H, p.tasks)
+    ref64 = oracle.spmm_mean_f64(g.row_ptr, g.col_idx, g.val, H)
+    return ref32, ref64
+
+
+def custom_graph(rp, ci, val=None):
+    rp = np.asarray(rp, np.int32)
+    ci = np.asarray(ci, np.int32)
+    val = np.ones(len(ci), np.float32) if val is None else np.asarray(val, np.float32)
+    return synth.Graph(len(rp) - 1, rp, ci, val)
+
+
+# --------------------------------------------------------------- small configs
+@pytest.mark.parametrize("cfg", [1, 2, 3, 4, 5])
+@pytest.mark.parametrize("which", [0, 1, 2])
+def test_small_config_candidates(gpu_ctx, cfg, which):
+    """Each configuration family at reduced size, at the three wave-based S."""
+    g = workloads.small(cfg)
+    K = workloads.FEATURE_DIM[cfg]
+    S = workloads.candidate_s(g.nnz, 256)[which]
+    p = problem(g, SKEWED_COSTS, S)
+    H = synth.features(g.n, K, workloads.FEATURE_SEED)
+    print(f"cfg={cfg} S={S} n={g.n} nnz={g.nnz} tasks={len(p.tasks)}", flush=True)
+    got, t = run_gpu(gpu_ctx, p, H)
+    ref32, ref64 = oracle_pair(p, g, H)
+    check(got, ref32)
+    check(got, ref64)
+    assert t.total_us > 0
+
+
+@pytest.mark.parametrize("S", [1, 2, 3, 7, 32, 1000])
+def test_small_rmat_segment_sizes(gpu_ctx, S):
+    """Heavy splitting (S=1) through no splitting (S=1000) on a skewed graph."""
+    g = workloads.small(4, seed=11)
+    H = synth.features(g.n, 128, 7)
+    p = problem(g, UNIT_COSTS, S)
+    got, _ = run_gpu(gpu_ctx, p, H)
+    ref32, ref64 = oracle_pair(p, g, H)
+    check(got, ref32)
+    check(got, ref64)
+
+
+def test_config1_full(gpu_ctx):
+    """The CPU plumbing configuration at full size (N=4,096, K=32)."""
+    g = workloads.graph(1)
+    H = synth.features(g.n, 32, workloads.FEATURE_SEED)
+    for S in workloads.candidate_s(g.nnz, 256):
+        p = problem(g, SKEWED_COSTS, S)
+        got, _ = run_gpu(gpu_ctx, p, H)
+        ref32, ref64 = oracle_pair(p, g, H)
+        check(got, ref32)
+        check(got, ref64)
+
+
+def test_config2_full(gpu_ctx):
+    """Chung-Lu N=1M K=64 at full size against the full CPU oracle."""
+    g = workloads.graph(2)
+    H = synth.features(g.n, 64, workloads.FEATURE_SEED)
+    S = workloads.candidate_s(g.nnz, 256)[0]
+    p = problem(g, SKEWED_COSTS, S)
+    got, _ = run_gpu(gpu_ctx, p, H)
+    ref32 = oracle.spmm_mean_f32(p.row_ptr, p.col_idx, p.val, p.origin, H, p.tasks)
+    check(got, ref32)
+
+
+# ------------------------------------------------------ full-size properties
+def features_rows(rows, K, seed):
+    """Host restatement of the feature generator for selected rows (numpy uint64)."""
+    def mix64(z):
+        z = z + np.uint64(0x9E3779B97F4A7C15)
+        z = (z ^ (z >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
+        z = (z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
+        return z ^ (z >> np.uint64(31))
+    with np.errstate(over="ignore"):
+        s = mix64(np.uint64(seed))
+        idx = (np.asarray(rows, np.uint64)[:, None] * np.uint64(K)
+               + np.arange(K, dtype=np.uint64)[None, :])
+        x = mix64(s + idx)
+    u = (x >> np.uint64(40)).astype(np.int64) - 8388608
+    return (u.astype(np.float32) * np.float32(2.0**-23)).astype(np.float32)
+
+
+def sampled_rows_check(g, C_dev, H_host, rng, n_sample=3000):
+    """Compare sampled rows (random + highest degree) with the fp64 closed form."""
+    torch = torch_mod()
+    deg = np.diff(g.row_ptr)
+    top = np.argsort(deg, kind="stable")[-200:]
+    rows = np.unique(np.concatenate([rng.integers(0, g.n, n_sample), top]))
+    got = C_dev[torch.from_numpy(rows).cuda()].cpu().numpy()
+    exp = np.zeros((len(rows), H_host.shape[1]), np.float64)
+    for i, r in enumerate(rows):
+        lo, hi = g.row_ptr[r], g.row_ptr[r + 1]
+        if hi > lo:
+            vals = g.val[lo:hi].astype(np.float64)
+            exp[i] = (vals[:, None] * H_host[g.col_idx[lo:hi]].astype(np.float64)).sum(0) / (hi - lo)
+    np.testing.assert_allclose(got, exp, rtol=RTOL, atol=ATOL)
+
+
+@pytest.mark.parametrize("cfg", [3, 4, 5])
+def test_full_config_properties(gpu_ctx, cfg):
+    torch = torch_mod()
+    g = workloads.graph(cfg)
+    K = workloads.FEATURE_DIM[cfg]
+    S = workloads.candidate_s(g.nnz, 256)[0]
+    p = problem(g, SKEWED_COSTS, S)
+    print(f"cfg={cfg} n={g.n} nnz={g.nnz} K={K} S={S} tasks={len(p.tasks)}", flush=True)
+    d_rp, d_ci, d_v, d_o = dev(p.row_ptr), dev(p.col_idx), dev(p.val), dev(p.origin)
+    d_t = dev(np.ascontiguousarray(p.tasks, np.int32).reshape(-1))
+    C = torch.full((g.n, K), float("nan"), dtype=torch.float32, device="cuda")
+    # All-ones features: every row with edges averages unit values to exactly 1.
+    ones = torch.ones((g.n, K), dtype=torch.float32, device="cuda")
+    gpu_ctx.spmm(d_rp, d_ci, d_v, d_o, g.n, g.nnz, ones, g.n, K, d_t, len(p.tasks), C)
+    deg = torch.from_numpy(np.diff(g.row_ptr)).cuda()
+    expect = (deg > 0).float()[:, None].expand(g.n, K)
+    assert torch.equal(C, expect) or torch.allclose(C, expect, rtol=RTOL, atol=ATOL)
+    del ones
+    # Seeded U[-1,1) features: sampled rows against the fp64 closed form.
+    H = torch.empty((g.n, K), dtype=torch.float32, device="cuda")
+    gpu_ctx.fill_features(H, g.n, K, workloads.FEATURE_SEED)
+    C.fill_(float("nan"))
+    t = gpu_ctx.spmm(d_rp, d_ci, d_v, d_o, g.n, g.nnz, H, g.n, K, d_t, len(p.tasks), C)
+    assert not torch.isnan(C).any().item()
+    H_host = synth.features(g.n, K, workloads.FEATURE_SEED)
+    sampled_rows_check(g, C, H_host, np.random.default_rng(cfg))
+    print(f"cfg={cfg} total_us={t.total_us:.1f} zero_us={t.zero_us:.1f}", flush=True)
+
+
+# ------------------------------------------------------------------ edge cases
+@pytest.mark.parametrize("K", [1, 2, 3, 4, 6, 12, 20, 36, 100, 128, 256, 260, 600, 1000, 1024])
+def test_feature_widths(gpu_ctx, K):
+    g = workloads.small(4, seed=3)
+    H = synth.features(g.n, K, 5)
+    p = problem(g, SKEWED_COSTS, 8)
+    got, _ = run_gpu(gpu_ctx, p, H)
+    ref32, ref64 = oracle_pair(p, g, H)
+    check(got, ref32)
+    check(got, ref64)
+
+
+@pytest.mark.parametrize("K", [1025, 1100, 2052, 4100])
+def test_large_k_entry(gpu_ctx, K):
+    """K above the work-group limit goes through the large-K entry point."""
+    g = workloads.small(1, seed=9)
+    H = synth.features(g.n, K, 5)
+    p = problem(g, UNIT_COSTS, 5)
+    got, _ = run_gpu(gpu_ctx, p, H, large_k=True)
+    ref32, ref64 = oracle_pair(p, g, H)
+    check(got, ref32)
+    check(got, ref64)
+    with pytest.raises(capi.CwlbError) as e:
+        run_gpu(gpu_ctx, p, H, large_k=False)
+    assert e.value.status == capi.INVALID_ARG
+
+
+def test_large_k_entry_rejects_small_k(gpu_ctx):
+    g = workloads.small(1, seed=9)
+    H = synth.features(g.n, 64, 5)
+    p = problem(g, UNIT_COSTS, 5)
+    with pytest.raises(capi.CwlbError) as e:
+        run_gpu(gpu_ctx, p, H, large_k=True)
+    assert e.value.status == capi.INVALID_ARG
+
+
+def test_hub_row_and_empty_rows(gpu_ctx, rng):
+    """One row of degree 5,000 among degree-0 and degree-1 rows, tiny S."""
+    n = 6000
+    deg = np.zeros(n, np.int64)
+    deg[17] = 5000
+    deg[rng.integers(0, n, 300)] = 1
+    rp = np.concatenate([[0], np.cumsum(deg)]).astype(np.int32)
+    ci = rng.integers(0, n, rp[-1]).astype(np.int32)
+    val = rng.uniform(-2, 2, rp[-1]).astype(np.float32)
+    g = custom_graph(rp, ci, val)
+    H = synth.features(n, 64, 1)
+    for S in (1, 2, 3, 64, 4999, 5000, 6000):
+        p = problem(g, UNIT_COSTS, S)
+        got, _ = run_gpu(gpu_ctx, p, H)
+        ref32, ref64 = oracle_pair(p, g, H)
+        check(got, ref32)
+        check(got, ref64)
+
+
+def test_all_rows_empty(gpu_ctx):
+    n = 1000
+    g = custom_graph(np.zeros(n + 1, np.int32), np.zeros(0, np.int32))
+    H = synth.features(n, 32, 1)
+    p = problem(g, UNIT_COSTS, 4)
+    got, _ = run_gpu(gpu_ctx, p, H)
+    assert np.array_equal(got, np.zeros((n, 32), np.float32))
+
+
+def test_duplicate_columns_and_values(gpu_ctx, rng):
+    """Repeated columns inside a row and non-unit values."""
+    n = 3000
+    deg = rng.integers(0, 40, n)
+    rp = np.concatenate([[0], np.cumsum(deg)]).astype(np.int32)
+    ci = rng.integers(0, 50, rp[-1]).astype(np.int32)
+    val = rng.normal(size=rp[-1]).astype(np.float32)
+    g = custom_graph(rp, ci, val)
+    H = synth.features(n, 64, 3)
+    for S in (2, 5, 17):
+        p = problem(g, SKEWED_COSTS, S)
+        got, _ = run_gpu(gpu_ctx, p, H)
+        ref32, ref64 = oracle_pair(p, g, H)
+        check(got, ref32)
+        check(got, ref64)
+
+
+def test_unsorted_graph_custom_tasks(gpu_ctx, rng):
+    """Caller-made task lists: one task per row, and whole-graph tasks."""
+    g = workloads.small(2, seed=5)
+    H = synth.features(g.n, 32, 3)
+    origin, rp, ci, val = capi.reorder_by_degree(g.row_ptr, g.col_idx, g.val)
+    base = workloads.Prepared(g.n, g.nnz, origin, rp, ci, val, None, 0, 0.0)
+    per_row = np.stack([np.arange(g.n), np.arange(1, g.n + 1), np.zeros(g.n), np.zeros(g.n)],
+                       1).astype(np.int32)
+    whole = np.array([[0, g.n, 0, 0]], np.int32)
+    for tasks in (per_row, whole):
+        base.tasks = tasks
+        got, _ = run_gpu(gpu_ctx, base, H)
+        ref32 = oracle.spmm_mean_f32(rp, ci, val, origin, H, tasks)
+        check(got, ref32)
+
+
+def test_zero_output_flag_with_partial_cover(gpu_ctx):
+    """ZERO_OUTPUT reproduces the reference's zeroed C for rows no task touches."""
+    g = workloads.small(1, seed=2)
+    H = synth.features(g.n, 32, 3)
+    p = problem(g, UNIT_COSTS, 6)
+    p.tasks = p.tasks[: len(p.tasks) // 2].copy()
+    got, _ = run_gpu(gpu_ctx, p, H, flags=capi.ZERO_OUTPUT)
+    ref32 = oracle.spmm_mean_f32(p.row_ptr, p.col_idx, p.val, p.origin, H, p.tasks)
+    check(got, ref32)
+
+
+def test_no_tasks_and_zero_k(gpu_ctx):
+    g = workloads.small(1, seed=2)
+    H = synth.features(g.n, 32, 3)
+    p = problem(g, UNIT_COSTS, 6)
+    p.tasks = np.zeros((0, 4), np.int32)
+    got, t = run_gpu(gpu_ctx, p, H, flags=capi.ZERO_OUTPUT)
+    assert np.array_equal(got, np.zeros_like(got))
+    assert t.total_us == 0.0
+    p2 = problem(g, UNIT_COSTS, 6)
+    got, t = run_gpu(gpu_ctx, p2, np.zeros((g.n, 0), np.float32))
+    assert got.shape == (g.n, 0) and t.total_us == 0.0
+
+
+def test_empty_graph(gpu_ctx):
+    g = custom_graph(np.zeros(1, np.int32), np.zeros(0, np.int32))
+    p = problem(g, UNIT_COSTS, 4)
+    assert len(p.tasks) == 0
+    got, t = run_gpu(gpu_ctx, p, np.zeros((0, 8), np.float32))
+    assert got.shape == (0, 8)
+
+
+def test_bad_column_index_is_reported(gpu_ctx):
+    """An out-of-range column is skipped on the device and reported."""
+    g = workloads.small(1, seed=2)
+    H = synth.features(g.n, 32, 3)
+    p = problem(g, UNIT_COSTS, 6)
+    p.col_idx = p.col_idx.copy()
+    p.col_idx[len(p.col_idx) // 2] = g.n + 5
+    with pytest.raises(capi.CwlbError) as e:
+        run_gpu(gpu_ctx, p, H)
+    assert e.value.status == capi.INVALID_ARG
+
+
+def test_host_pointer_entry(gpu_ctx):
+    g = workloads.small(4, seed=8)
+    H = synth.features(g.n, 128, 3)
+    p = problem(g, SKEWED_COSTS, 16)
+    got, t = gpu_ctx.spmm_host(p.row_ptr, p.col_idx, p.val, p.origin, H, p.tasks)
+    ref32, ref64 = oracle_pair(p, g, H)
+    check(got, ref32)
+    check(got, ref64)
+    assert t.main_us > 0
+
+
+def test_repeat_runs_stable(gpu_ctx):
+    """Full rows are written identically on every run; split rows within tolerance."""
+    g = workloads.small(4, seed=4)
+    H = synth.features(g.n, 128, 3)
+    p = problem(g, UNIT_COSTS, 4)
+    a, _ = run_gpu(gpu_ctx, p, H)
+    b, _ = run_gpu(gpu_ctx, p, H)
+    check(a, b)
+
+
+def test_device_features_match_host(gpu_ctx):
+    torch = torch_mod()
+    for rows, K in ((1000, 33), (257, 128), (1, 1)):
+        H = torch.empty((rows, K), dtype=torch.float32, device="cuda")
+        gpu_ctx.fill_features(H, rows, K, 42)
+        assert np.array_equal(H.cpu().numpy(), synth.features(rows, K, 42))
+        assert np.array_equal(features_rows(np.arange(rows), K, 42), synth.features(rows, K, 42))
