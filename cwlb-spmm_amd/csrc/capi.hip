@@ -128,7 +128,7 @@ cwlb_status cwlb_ctx_create(int device, void* stream, cwlb_ctx** out)
     c->wave = prop.warpSize;
     c->lds_per_block = prop.sharedMemPerBlock;
     c->total_mem = prop.totalGlobalMem;
-    std::snprintf(c->name, sizeof c->name, "%s", prop.name);
+    std::snprintf(c->name, sizeof c->name, "%s", prop.name[0] ? prop.name : prop.gcnArchName);
     std::snprintf(c->arch, sizeof c->arch, "%s", prop.gcnArchName);
     hipError_t e = hipSuccess;
     for (auto& ev : c->ev)
