@@ -56,6 +56,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--costs", default=COST_FILE, help="cost file (four coefficients)")
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="also run one device-to-device copy of this many MiB (a known-size "
+                         "reference for the HBM traffic counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
@@ -124,7 +127,22 @@ def main():
     times = [call(d_t, T, True) for _ in range(args.steps)]
     main_us = float(np.mean([t.main_us for t in times]))
     zero_us = float(np.mean([t.zero_us for t in times]))
+    # The reference's structure (one task per wave, one atomic add per
+    # partial segment), for comparison.
+    pt = [ctx.spmm(d_rp, d_ci, d_v, d_o, g.n, g.nnz, H, g.n, K, d_t, T, C,
+                   flags=capi.PER_TASK) for _ in range(10)]
+    per_task_us = float(np.mean([t.total_us for t in pt]))
     log(f"S={S} T={T} ms/step={ms_per_step:.3f} main_us={main_us:.1f} zero_us={zero_us:.1f}")
+
+    if args.copy_probe_mib:
+        nb = args.copy_probe_mib << 20
+        src = torch.ones(nb // 4, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"copy probe: {nb} bytes read and written")
+        del src, dst
 
     flops = 2.0 * g.nnz * K
     gflops = flops / (ms_per_step * 1e-3) / 1e9
@@ -176,6 +194,7 @@ def main():
         "config": {"workload": workloads.NAMES[cfg], "n": g.n, "nnz": g.nnz, "K": K, "S": S,
                    "tasks": T, "costs": list(costs), "device": info.name.decode(),
                    "main_kernel_us": round(main_us, 2), "zero_pass_us": round(zero_us, 2),
+                   "per_task_mode_us": round(per_task_us, 2),
                    "algorithmic_bytes": b_alg},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),

@@ -67,10 +67,11 @@ cwlb_status run_spmm(cwlb_ctx* ctx, const SpmmArgs& a, uint32_t flags, cwlb_timi
     if (st != CWLB_OK) return st;
     DeviceGuard g(ctx->device);
     const bool zero_all = (flags & CWLB_SPMM_ZERO_OUTPUT) != 0;
+    const bool per_task = (flags & CWLB_SPMM_PER_TASK) != 0;
     if (a.K == 0 || a.n_tasks == 0) {
         // The reference returns a zero matrix and time 0 (parallelMatrix.cpp:80-83, 101-104).
         if (zero_all && a.n_rows > 0 && a.K > 0) {
-            st = launch_spmm_mean(ctx, a, true, false);
+            st = launch_spmm_mean(ctx, a, true, per_task, false);
             if (st != CWLB_OK) return st;
         }
         if (timing) {
@@ -79,7 +80,7 @@ cwlb_status run_spmm(cwlb_ctx* ctx, const SpmmArgs& a, uint32_t flags, cwlb_timi
         }
         return CWLB_OK;
     }
-    st = launch_spmm_mean(ctx, a, zero_all, timing != nullptr);
+    st = launch_spmm_mean(ctx, a, zero_all, per_task, timing != nullptr);
     if (st != CWLB_OK) return st;
     if (timing) return finish_timed(ctx, timing);
     return CWLB_OK;
@@ -180,6 +181,19 @@ cwlb_status cwlb_ctx_device_info(cwlb_ctx* ctx, cwlb_device_info* out)
     out->total_global_mem = static_cast<int64_t>(ctx->total_mem);
     std::snprintf(out->name, sizeof out->name, "%s", ctx->name);
     std::snprintf(out->arch, sizeof out->arch, "%s", ctx->arch);
+    return CWLB_OK;
+}
+
+cwlb_status cwlb_ctx_set_schedule(cwlb_ctx* ctx, int32_t tasks_per_wave, int32_t feature_slices)
+{
+    if (!ctx) return fail(CWLB_INVALID_ARG, "null context");
+    if (tasks_per_wave < 0)
+        return fail(CWLB_INVALID_ARG, "tasks_per_wave must be >= 0 (0 = automatic)");
+    if (feature_slices != 0 && feature_slices != 1 && feature_slices != 2 && feature_slices != 4 &&
+        feature_slices != 8)
+        return fail(CWLB_INVALID_ARG, "feature_slices must be 0, 1, 2, 4 or 8");
+    ctx->sched_tasks_per_wave = tasks_per_wave;
+    ctx->sched_slices = feature_slices;
     return CWLB_OK;
 }
 

@@ -22,6 +22,9 @@ struct cwlb_ctx {
     // Device status word written by the kernels: bit 0 = a column index was
     // outside [0, h_rows), bit 1 = an origin entry was outside [0, n_rows).
     int* d_status = nullptr;
+    // Schedule overrides (0 = automatic): tasks per wave, feature slices.
+    int sched_tasks_per_wave = 0;
+    int sched_slices = 0;
 };
 
 namespace cwlb {
@@ -68,7 +71,9 @@ struct SpmmArgs {
 
 // Enqueues the split-row clearing pass (or the full clear when zero_all)
 // and the aggregation kernel on ctx->stream, bracketed by ctx->ev[0..2].
-cwlb_status launch_spmm_mean(cwlb_ctx* ctx, const SpmmArgs& a, bool zero_all, bool record_events);
+// per_task runs one task per wave (no task-run fusion, no feature slices).
+cwlb_status launch_spmm_mean(cwlb_ctx* ctx, const SpmmArgs& a, bool zero_all, bool per_task,
+                             bool record_events);
 
 cwlb_status launch_fill_features(cwlb_ctx* ctx, float* H, int64_t rows, int32_t K, uint64_t seed);
 

@@ -10,19 +10,29 @@
 // (the reference leaves its host-zeroed C untouched there).
 //
 // Mapping to CDNA4 (64-lane waves):
-//   * one wave executes one task; a block holds kWaves waves (kWaves tasks);
-//   * a row of K floats is covered by a "slot" of G lanes, each lane holding
-//     R vectors of VEC floats (128-bit loads when K % 4 == 0); a wave has
-//     NS = 64 / G slots;
+//   * a wave executes a run of M consecutive tasks (M = 1 reproduces the
+//     reference's one task per work-group).  Consecutive tasks tile the
+//     nonzeros contiguously, so a run is itself the task
+//     (row_start of its first task, row_end of its last, first_row_offset of
+//     its first, last_row_nnz of its last); a row split only between tasks
+//     of the same run is reduced in registers and stored instead of being
+//     added atomically segment by segment;
+//   * a row slice of Ks = K / SL floats is covered by a "slot" of G lanes,
+//     each lane holding R vectors of VEC floats (128-bit loads when
+//     K % 4 == 0); a wave has NS = 64 / G slots.  With SL > 1 the feature
+//     slices are spread over the XCDs (work-groups are dispatched to the 8
+//     XCDs round-robin), so each XCD's L2 caches one slice of the hot
+//     feature rows and holds SL times as many of them;
 //   * short rows run row-per-slot, RU rows per slot at a time, each row
 //     summed sequentially in CSR order (bit-identical to the reference's
 //     per-work-item loop);
 //   * a long chunk runs on all slots at once, UL nonzeros in flight per
 //     slot, followed by a shuffle reduction across slots;
 //   * column indices and values are fetched 64 at a time with one coalesced
-//     load and handed to the slots with cross-lane shuffles.
-// Split rows are cleared by zero_first_segments before the main kernel, in
-// the task that owns their first segment, so each is cleared exactly once.
+//     streaming load and handed to the slots with cross-lane shuffles; C is
+//     written with streaming stores.
+// Split rows are cleared by zero_first_segments before the main kernel, by
+// the run that owns their first segment, so each is cleared exactly once.
 #include "internal.h"
 
 #include <algorithm>
@@ -68,6 +78,13 @@ template <int VEC>
 __device__ __forceinline__ void vstore(float* p, typename VecT<VEC>::T v)
 {
     *reinterpret_cast<typename VecT<VEC>::T*>(p) = v;
+}
+
+// Streaming (non-temporal) store: C is written once and not re-read.
+template <int VEC>
+__device__ __forceinline__ void vstore_nt(float* p, typename VecT<VEC>::T v)
+{
+    __builtin_nontemporal_store(v, reinterpret_cast<typename VecT<VEC>::T*>(p));
 }
 
 __device__ __forceinline__ float vfma(float a, float h, float c) { return __builtin_fmaf(a, h, c); }
@@ -179,13 +196,49 @@ __device__ __forceinline__ Chunk row_chunk(const int* __restrict__ rp, int r, in
 
 constexpr int cmin(int a, int b) { return a < b ? a : b; }
 
-template <int VEC, int G, int R, int U>
+// Bounds of run `run` (tasks [run*M, min(run*M + M, n_tasks))) as one task.
+struct RunTask {
+    int rs, re, fo, ln;
+};
+
+__device__ __forceinline__ RunTask run_task(const cwlb_task* __restrict__ tasks,
+                                            long long n_tasks, long long run, int M)
+{
+    const long long t0 = run * M;
+    const long long tl = (t0 + M <= n_tasks ? t0 + M : n_tasks) - 1;
+    const cwlb_task a = tasks[t0];
+    RunTask r;
+    r.rs = a.row_start;
+    r.fo = a.first_row_offset;
+    if (tl == t0) {
+        r.re = a.row_end;
+        r.ln = a.last_row_nnz;
+    } else {
+        const cwlb_task z = tasks[tl];
+        r.re = z.row_end;
+        r.ln = z.last_row_nnz;
+    }
+    return r;
+}
+
+// Block b runs on XCD b % 8; slice = XCD % SL, and the blocks of one slice
+// enumerate the run blocks 0, 1, 2, ... (a bijection for SL in {1, 2, 4, 8}).
+template <int SL>
+__device__ __forceinline__ void block_slice(int& slice, long long& jb)
+{
+    const int bx = blockIdx.x;
+    const int xcd = bx & 7;
+    slice = xcd % SL;
+    jb = static_cast<long long>(bx >> 3) * (8 / SL) + xcd / SL;
+}
+
+template <int VEC, int G, int R, int U, int SL>
 __global__ void __launch_bounds__(kBlock)
-spmm_mean_tasks(const int* __restrict__ rp, const int* __restrict__ ci,
-                const float* __restrict__ val, const int* __restrict__ origin, int n_rows,
-                long long nnz, const float* __restrict__ H, long long h_rows, int K,
-                const cwlb_task* __restrict__ tasks, long long n_tasks, float* __restrict__ C,
-                int* __restrict__ status)
+spmm_mean_runs(const int* __restrict__ rp, const int* __restrict__ ci,
+               const float* __restrict__ val, const int* __restrict__ origin, int n_rows,
+               long long nnz, const float* __restrict__ H, long long h_rows, int ld,
+               const cwlb_task* __restrict__ tasks, long long n_tasks, int M, long long n_runs,
+               long long n_blocks, float* __restrict__ C, int* __restrict__ status)
 {
     using V = typename VecT<VEC>::T;
     constexpr int NS = 64 / G;                     // row slots per wave
@@ -198,17 +251,23 @@ spmm_mean_tasks(const int* __restrict__ rp, const int* __restrict__ ci,
     const int lane = threadIdx.x & 63;
     const int slot = lane / G;
     const int sub = lane - slot * G;
-    const long long t = static_cast<long long>(blockIdx.x) * kWaves +
-                        __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    if (t >= n_tasks) return;
+    int slice;
+    long long jb;
+    block_slice<SL>(slice, jb);
+    if (jb >= n_blocks) return;
+    const long long run = jb * kWaves + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if (run >= n_runs) return;
 
-    const cwlb_task tk = tasks[t];
-    const int rs = tk.row_start;
-    const int re = tk.row_end;
-    const int fo = tk.first_row_offset;
-    const int ln = tk.last_row_nnz;
+    const RunTask tk = run_task(tasks, n_tasks, run, M);
+    const int rs = tk.rs;
+    const int re = tk.re;
+    const int fo = tk.fo;
+    const int ln = tk.ln;
     const int rlo = max(rs, 0);
     const int rhi = min(re, n_rows);
+    const int K = ld / SL;                       // features of this slice
+    const float* __restrict__ Hs = H + slice * K;
+    float* __restrict__ Cs = C + slice * K;
     const int F = K / VEC;
     const int npass = (F + G * R - 1) / (G * R);
     int bad = 0;
@@ -229,8 +288,8 @@ spmm_mean_tasks(const int* __restrict__ rp, const int* __restrict__ ci,
                     int colw = 0;
                     float valw = 0.0f;
                     if (lane < wn) {
-                        colw = ci[c0.base + w0 + lane];
-                        valw = val[c0.base + w0 + lane];
+                        colw = __builtin_nontemporal_load(ci + c0.base + w0 + lane);
+                        valw = __builtin_nontemporal_load(val + c0.base + w0 + lane);
                     }
                     for (int k0 = 0; k0 < wn; k0 += STEP) {
                         int cc[UL];
@@ -251,7 +310,7 @@ spmm_mean_tasks(const int* __restrict__ rp, const int* __restrict__ ci,
                         V h[UL][R];
 #pragma unroll
                         for (int u = 0; u < UL; ++u) {
-                            const float* hrow = H + static_cast<size_t>(cc[u]) * K;
+                            const float* hrow = Hs + static_cast<size_t>(cc[u]) * ld;
 #pragma unroll
                             for (int q = 0; q < R; ++q) {
                                 const int f = fl + G * q;
@@ -277,7 +336,7 @@ spmm_mean_tasks(const int* __restrict__ rp, const int* __restrict__ ci,
                 if (static_cast<unsigned>(o) >= static_cast<unsigned>(n_rows)) {
                     bad |= 2;
                 } else if (slot == 0) {
-                    float* crow = C + static_cast<size_t>(o) * K;
+                    float* crow = Cs + static_cast<size_t>(o) * ld;
                     const float fd = static_cast<float>(c0.d);
                     const bool full = (c0.b == 0 && c0.e == c0.d);
 #pragma unroll
@@ -286,7 +345,7 @@ spmm_mean_tasks(const int* __restrict__ rp, const int* __restrict__ ci,
                         if (f < F) {
                             const V res = vdiv(acc[q], fd);
                             if (full)
-                                vstore<VEC>(crow + f * VEC, res);
+                                vstore_nt<VEC>(crow + f * VEC, res);
                             else
                                 vatomic_add(crow + f * VEC, res);
                         }
@@ -313,8 +372,8 @@ spmm_mean_tasks(const int* __restrict__ rp, const int* __restrict__ ci,
             int colw = 0;
             float valw = 0.0f;
             if (win && lane < ge - gs && gs >= 0 && static_cast<long long>(gs) + lane < nnz) {
-                colw = ci[gs + lane];
-                valw = val[gs + lane];
+                colw = __builtin_nontemporal_load(ci + gs + lane);
+                valw = __builtin_nontemporal_load(val + gs + lane);
             }
             V acc[RU][R];
             int pos[RU];
@@ -356,7 +415,7 @@ spmm_mean_tasks(const int* __restrict__ rp, const int* __restrict__ ci,
                 V h[RU][R];
 #pragma unroll
                 for (int u = 0; u < RU; ++u) {
-                    const float* hrow = H + static_cast<size_t>(cc[u]) * K;
+                    const float* hrow = Hs + static_cast<size_t>(cc[u]) * ld;
 #pragma unroll
                     for (int q = 0; q < R; ++q) {
                         const int f = fl + G * q;
@@ -383,12 +442,12 @@ spmm_mean_tasks(const int* __restrict__ rp, const int* __restrict__ ci,
                         bad |= 2;
                         continue;
                     }
-                    float* crow = C + static_cast<size_t>(o) * K;
+                    float* crow = Cs + static_cast<size_t>(o) * ld;
                     if (d <= 0) {
 #pragma unroll
                         for (int q = 0; q < R; ++q) {
                             const int f = fl + G * q;
-                            if (f < F) vstore<VEC>(crow + f * VEC, vzero<VEC>());
+                            if (f < F) vstore_nt<VEC>(crow + f * VEC, vzero<VEC>());
                         }
                     } else if (e > b) {
                         const float fd = static_cast<float>(d);
@@ -399,7 +458,7 @@ spmm_mean_tasks(const int* __restrict__ rp, const int* __restrict__ ci,
                             if (f < F) {
                                 const V res = vdiv(acc[u][q], fd);
                                 if (full)
-                                    vstore<VEC>(crow + f * VEC, res);
+                                    vstore_nt<VEC>(crow + f * VEC, res);
                                 else
                                     vatomic_add(crow + f * VEC, res);
                             }
@@ -414,30 +473,29 @@ spmm_mean_tasks(const int* __restrict__ rp, const int* __restrict__ ci,
 }
 
 // Clears, once each, the C rows that receive atomic partial sums: a row is
-// cleared by the task whose chunk of it starts at nonzero 0 without reaching
-// the row's end.  One lane per task; the wave then clears the marked rows
-// with coalesced stores.  Block 0 also resets the status word.
+// cleared by the run whose chunk of it starts at nonzero 0 without reaching
+// the row's end (only a run's first and last rows can be partial).  One lane
+// per run; the wave then clears the marked rows with coalesced stores.
+// Block 0 also resets the status word.
 template <int VEC>
 __global__ void __launch_bounds__(kBlock)
 zero_first_segments(const int* __restrict__ rp, const int* __restrict__ origin, int n_rows,
-                    long long nnz, const cwlb_task* __restrict__ tasks, long long n_tasks,
-                    int K, float* __restrict__ C, int* __restrict__ status)
+                    long long nnz, const cwlb_task* __restrict__ tasks, long long n_tasks, int M,
+                    long long n_runs, int K, float* __restrict__ C, int* __restrict__ status)
 {
     const int lane = threadIdx.x & 63;
-    const long long t = static_cast<long long>(blockIdx.x) * kBlock + threadIdx.x;
+    const long long run = static_cast<long long>(blockIdx.x) * kBlock + threadIdx.x;
     if (blockIdx.x == 0 && threadIdx.x == 0) *status = 0;
     int o1 = -1, o2 = -1;
-    if (t < n_tasks) {
-        const cwlb_task tk = tasks[t];
-        const int rlo = max(tk.row_start, 0);
-        const int rhi = min(tk.row_end, n_rows);
+    if (run < n_runs) {
+        const RunTask tk = run_task(tasks, n_tasks, run, M);
+        const int rlo = max(tk.rs, 0);
+        const int rhi = min(tk.re, n_rows);
         if (rlo < rhi) {
-            const Chunk a = row_chunk(rp, rlo, tk.row_start, tk.row_end, tk.first_row_offset,
-                                      tk.last_row_nnz, nnz);
+            const Chunk a = row_chunk(rp, rlo, tk.rs, tk.re, tk.fo, tk.ln, nnz);
             if (a.d > 0 && a.b == 0 && a.e > 0 && a.e < a.d) o1 = origin[rlo];
             if (rhi - 1 != rlo) {
-                const Chunk z = row_chunk(rp, rhi - 1, tk.row_start, tk.row_end,
-                                          tk.first_row_offset, tk.last_row_nnz, nnz);
+                const Chunk z = row_chunk(rp, rhi - 1, tk.rs, tk.re, tk.fo, tk.ln, nnz);
                 if (z.d > 0 && z.b == 0 && z.e > 0 && z.e < z.d) o2 = origin[rhi - 1];
             }
         }
@@ -507,54 +565,78 @@ unsigned long long host_mix64(unsigned long long z)
     return z ^ (z >> 31);
 }
 
-template <int VEC, int G, int R>
-void launch_main(hipStream_t st, const SpmmArgs& a, int* status)
+// Launch geometry of one call: M tasks per wave, SL feature slices.
+struct Plan {
+    int vec;
+    int sl;
+    int M;
+    long long runs;
+    long long blocks;      // run blocks per slice
+    long long grid;        // launched blocks (slices x run blocks, padded to 8)
+};
+
+template <int VEC, int G, int R, int SL>
+void launch_main(hipStream_t st, const SpmmArgs& a, const Plan& p, int* status)
 {
     constexpr int U = (R == 1) ? 8 : (R == 2) ? 4 : (R <= 4) ? 2 : 1;
-    const long long blocks = (a.n_tasks + kWaves - 1) / kWaves;
-    hipLaunchKernelGGL((spmm_mean_tasks<VEC, G, R, U>), dim3(static_cast<unsigned>(blocks)),
+    hipLaunchKernelGGL((spmm_mean_runs<VEC, G, R, U, SL>), dim3(static_cast<unsigned>(p.grid)),
                        dim3(kBlock), 0, st, a.row_ptr, a.col_idx, a.val, a.origin, a.n_rows,
                        static_cast<long long>(a.nnz), a.H, static_cast<long long>(a.h_rows), a.K,
-                       a.tasks, static_cast<long long>(a.n_tasks), a.C, status);
+                       a.tasks, static_cast<long long>(a.n_tasks), p.M, p.runs, p.blocks, a.C,
+                       status);
 }
 
-template <int VEC>
-void dispatch_main(hipStream_t st, const SpmmArgs& a, int* status)
+template <int VEC, int SL>
+void dispatch_width(hipStream_t st, const SpmmArgs& a, const Plan& p, int* status)
 {
-    const int F = a.K / VEC;
+    const int F = a.K / SL / VEC;
     if (F <= 64) {
         int G = 1;
         while (G < F) G <<= 1;
         switch (G) {
-        case 1: return launch_main<VEC, 1, 1>(st, a, status);
-        case 2: return launch_main<VEC, 2, 1>(st, a, status);
-        case 4: return launch_main<VEC, 4, 1>(st, a, status);
-        case 8: return launch_main<VEC, 8, 1>(st, a, status);
-        case 16: return launch_main<VEC, 16, 1>(st, a, status);
-        case 32: return launch_main<VEC, 32, 1>(st, a, status);
-        default: return launch_main<VEC, 64, 1>(st, a, status);
+        case 1: return launch_main<VEC, 1, 1, SL>(st, a, p, status);
+        case 2: return launch_main<VEC, 2, 1, SL>(st, a, p, status);
+        case 4: return launch_main<VEC, 4, 1, SL>(st, a, p, status);
+        case 8: return launch_main<VEC, 8, 1, SL>(st, a, p, status);
+        case 16: return launch_main<VEC, 16, 1, SL>(st, a, p, status);
+        case 32: return launch_main<VEC, 32, 1, SL>(st, a, p, status);
+        default: return launch_main<VEC, 64, 1, SL>(st, a, p, status);
         }
     }
-    const int R = std::min((F + 63) / 64, 8);
-    switch (R) {
-    case 2: return launch_main<VEC, 64, 2>(st, a, status);
-    case 3: return launch_main<VEC, 64, 3>(st, a, status);
-    case 4: return launch_main<VEC, 64, 4>(st, a, status);
-    case 5: return launch_main<VEC, 64, 5>(st, a, status);
-    case 6: return launch_main<VEC, 64, 6>(st, a, status);
-    case 7: return launch_main<VEC, 64, 7>(st, a, status);
-    default: return launch_main<VEC, 64, 8>(st, a, status);
+    if constexpr (SL != 1) {
+        // Wider slices than one wave: the kernel loops over feature passes.
+        return launch_main<VEC, 64, 1, SL>(st, a, p, status);
+    } else {
+        const int R = std::min((F + 63) / 64, 8);
+        switch (R) {
+        case 2: return launch_main<VEC, 64, 2, 1>(st, a, p, status);
+        case 3: return launch_main<VEC, 64, 3, 1>(st, a, p, status);
+        case 4: return launch_main<VEC, 64, 4, 1>(st, a, p, status);
+        case 5: return launch_main<VEC, 64, 5, 1>(st, a, p, status);
+        case 6: return launch_main<VEC, 64, 6, 1>(st, a, p, status);
+        case 7: return launch_main<VEC, 64, 7, 1>(st, a, p, status);
+        default: return launch_main<VEC, 64, 8, 1>(st, a, p, status);
+        }
     }
 }
 
 template <int VEC>
-void launch_zero(hipStream_t st, const SpmmArgs& a, int* status)
+void dispatch_main(hipStream_t st, const SpmmArgs& a, const Plan& p, int* status)
 {
-    const long long blocks = (a.n_tasks + kBlock - 1) / kBlock;
+    if (p.sl == 8) return dispatch_width<VEC, 8>(st, a, p, status);
+    if (p.sl == 4) return dispatch_width<VEC, 4>(st, a, p, status);
+    if (p.sl == 2) return dispatch_width<VEC, 2>(st, a, p, status);
+    return dispatch_width<VEC, 1>(st, a, p, status);
+}
+
+template <int VEC>
+void launch_zero(hipStream_t st, const SpmmArgs& a, const Plan& p, int* status)
+{
+    const long long blocks = (p.runs + kBlock - 1) / kBlock;
     hipLaunchKernelGGL(zero_first_segments<VEC>, dim3(static_cast<unsigned>(blocks)),
                        dim3(kBlock), 0, st, a.row_ptr, a.origin, a.n_rows,
-                       static_cast<long long>(a.nnz), a.tasks,
-                       static_cast<long long>(a.n_tasks), a.K, a.C, status);
+                       static_cast<long long>(a.nnz), a.tasks, static_cast<long long>(a.n_tasks),
+                       p.M, p.runs, a.K, a.C, status);
 }
 
 int pick_vec(const SpmmArgs& a)
@@ -566,37 +648,67 @@ int pick_vec(const SpmmArgs& a)
     return 1;
 }
 
+// Tasks per wave: enough runs for ~64 waves per CU, at most 64 tasks each.
+// Feature slices across XCDs: only with runs long enough to amortise the
+// per-run setup (M >= 8), and only when each slice is a whole number of
+// 128-byte lines.  The context's schedule overrides either choice.
+Plan make_plan(const cwlb_ctx* ctx, const SpmmArgs& a, bool per_task)
+{
+    Plan p{};
+    p.vec = pick_vec(a);
+    p.M = 1;
+    p.sl = 1;
+    if (!per_task) {
+        if (ctx->sched_tasks_per_wave > 0) {
+            p.M = ctx->sched_tasks_per_wave;
+        } else {
+            const long long target = static_cast<long long>(std::max(ctx->compute_units, 1)) * 64;
+            p.M = static_cast<int>(
+                std::max<long long>(1, std::min<long long>(64, a.n_tasks / target)));
+        }
+        if (ctx->sched_slices > 0) {
+            p.sl = ctx->sched_slices;
+        } else if (p.M >= 8) {
+            if (a.K % 128 == 0 && a.K >= 128 && a.K <= 512) p.sl = 4;
+            else if (a.K % 64 == 0 && a.K >= 64 && a.K <= 256) p.sl = 2;
+        }
+        if (p.vec != 4 || a.K % (4 * p.sl) != 0) p.sl = 1;
+    }
+    p.runs = (a.n_tasks + p.M - 1) / p.M;
+    p.blocks = (p.runs + kWaves - 1) / kWaves;
+    p.grid = p.sl == 1 ? p.blocks : (p.blocks * p.sl + 7) / 8 * 8;
+    return p;
+}
+
 }  // namespace
 
-cwlb_status launch_spmm_mean(cwlb_ctx* ctx, const SpmmArgs& a, bool zero_all, bool record_events)
+cwlb_status launch_spmm_mean(cwlb_ctx* ctx, const SpmmArgs& a, bool zero_all, bool per_task,
+                             bool record_events)
 {
     hipStream_t st = ctx->stream;
     if (record_events) CWLB_HIP_TRY(hipEventRecord(ctx->ev[0], st));
     const long long total = static_cast<long long>(a.n_rows) * a.K;
     if (zero_all) {
-        if (total > 0) {
-            const long long want = (total / 4 + kBlock - 1) / kBlock;
-            const unsigned blocks = static_cast<unsigned>(std::max<long long>(1, std::min<long long>(want, 65536)));
-            hipLaunchKernelGGL(fill_zero, dim3(blocks), dim3(kBlock), 0, st, a.C, total,
-                               ctx->d_status);
-        } else {
-            hipLaunchKernelGGL(fill_zero, dim3(1), dim3(kBlock), 0, st, a.C, 0LL, ctx->d_status);
-        }
+        const long long want = (total / 4 + kBlock - 1) / kBlock;
+        const unsigned blocks =
+            static_cast<unsigned>(std::max<long long>(1, std::min<long long>(want, 65536)));
+        hipLaunchKernelGGL(fill_zero, dim3(blocks), dim3(kBlock), 0, st, a.C,
+                           std::max<long long>(total, 0), ctx->d_status);
     }
-    const int vec = pick_vec(a);
+    const Plan p = make_plan(ctx, a, per_task);
     if (!zero_all && a.n_tasks > 0 && a.K > 0) {
-        if (vec == 4) launch_zero<4>(st, a, ctx->d_status);
-        else if (vec == 2) launch_zero<2>(st, a, ctx->d_status);
-        else launch_zero<1>(st, a, ctx->d_status);
+        if (p.vec == 4) launch_zero<4>(st, a, p, ctx->d_status);
+        else if (p.vec == 2) launch_zero<2>(st, a, p, ctx->d_status);
+        else launch_zero<1>(st, a, p, ctx->d_status);
     } else if (!zero_all) {
         hipLaunchKernelGGL(fill_zero, dim3(1), dim3(kBlock), 0, st, a.C, 0LL, ctx->d_status);
     }
     CWLB_HIP_TRY(hipGetLastError());
     if (record_events) CWLB_HIP_TRY(hipEventRecord(ctx->ev[1], st));
     if (a.n_tasks > 0 && a.K > 0) {
-        if (vec == 4) dispatch_main<4>(st, a, ctx->d_status);
-        else if (vec == 2) dispatch_main<2>(st, a, ctx->d_status);
-        else dispatch_main<1>(st, a, ctx->d_status);
+        if (p.vec == 4) dispatch_main<4>(st, a, p, ctx->d_status);
+        else if (p.vec == 2) dispatch_main<2>(st, a, p, ctx->d_status);
+        else dispatch_main<1>(st, a, p, ctx->d_status);
         CWLB_HIP_TRY(hipGetLastError());
     }
     if (record_events) CWLB_HIP_TRY(hipEventRecord(ctx->ev[2], st));

@@ -99,6 +99,14 @@ cwlb_status cwlb_ctx_destroy(cwlb_ctx* ctx);
 cwlb_status cwlb_ctx_set_stream(cwlb_ctx* ctx, void* stream);
 cwlb_status cwlb_ctx_synchronize(cwlb_ctx* ctx);
 cwlb_status cwlb_ctx_device_info(cwlb_ctx* ctx, cwlb_device_info* out);
+/* Schedule of later SpMM calls on this context: tasks executed per wave
+ * (a run of consecutive tasks) and feature slices spread across the XCDs.
+ * 0 selects automatically (the default).  feature_slices must be 0, 1, 2, 4
+ * or 8; a slice count that does not split K into multiples of 4 floats (or
+ * with misaligned H / C) falls back to 1.  CWLB_SPMM_PER_TASK overrides both
+ * with 1.  No counterpart in the reference (its work-group per task is
+ * fixed); tuning and tests use it. */
+cwlb_status cwlb_ctx_set_schedule(cwlb_ctx* ctx, int32_t tasks_per_wave, int32_t feature_slices);
 
 /* ------------------------------------------------------------ aggregation
  * C[Origin_local[r]][k] = (sum over the task chunks of row r of
@@ -129,6 +137,14 @@ cwlb_status cwlb_ctx_device_info(cwlb_ctx* ctx, cwlb_device_info* out);
  * cwlb_spmm_mean_f32_large_k mirrors spmmKernelLargeKFallback: it requires
  * K > max work-group size (parallelMatrix.cpp:287-290). */
 #define CWLB_SPMM_ZERO_OUTPUT 0x1u
+/* Execute exactly one task per wave, each partial chunk added atomically
+ * (the reference's structure).  Without this flag a wave executes a run of
+ * consecutive tasks, chosen from the task count and the CU count; a run is
+ * itself a task (the union of consecutive tasks is contiguous), so rows
+ * split only inside a run are reduced in registers and stored, and the
+ * feature columns may be split across the XCDs.  Both modes give the same
+ * result up to float rounding. */
+#define CWLB_SPMM_PER_TASK 0x2u
 
 cwlb_status cwlb_spmm_mean_f32(cwlb_ctx* ctx, const int32_t* row_ptr, const int32_t* col_idx,
                                const float* val, const int32_t* origin, int32_t n_rows,

@@ -50,6 +50,21 @@ def run_gpu(ctx, p, H, flags=0, c_fill=float("nan"), large_k=False, h_dev=None):
     return C[:p.n, :K].cpu().numpy(), t
 
 
+# (tasks_per_wave, feature_slices, flags): automatic, the reference's one task
+# per wave, and forced task-run fusion / XCD feature slicing (small graphs do
+# not trigger them automatically).
+SCHEDULES = [(0, 0, 0), (0, 0, capi.PER_TASK), (3, 1, 0), (8, 2, 0), (16, 4, 0), (64, 4, 0)]
+SCHED_IDS = ["auto", "per_task", "m3", "m8s2", "m16s4", "m64s4"]
+
+
+@pytest.fixture(params=SCHEDULES, ids=SCHED_IDS)
+def sched(request, gpu_ctx):
+    m, sl, flags = request.param
+    gpu_ctx.set_schedule(m, sl)
+    yield flags
+    gpu_ctx.set_schedule(0, 0)
+
+
 def check(got, ref):
     np.testing.assert_allclose(got, ref, rtol=RTOL, atol=ATOL)
 
@@ -74,7 +89,7 @@ def custom_graph(rp, ci, val=None):
 # --------------------------------------------------------------- small configs
 @pytest.mark.parametrize("cfg", [1, 2, 3, 4, 5])
 @pytest.mark.parametrize("which", [0, 1, 2])
-def test_small_config_candidates(gpu_ctx, cfg, which):
+def test_small_config_candidates(gpu_ctx, sched, cfg, which):
     """Each configuration family at reduced size, at the three wave-based S."""
     g = workloads.small(cfg)
     K = workloads.FEATURE_DIM[cfg]
@@ -82,7 +97,7 @@ def test_small_config_candidates(gpu_ctx, cfg, which):
     p = problem(g, SKEWED_COSTS, S)
     H = synth.features(g.n, K, workloads.FEATURE_SEED)
     print(f"cfg={cfg} S={S} n={g.n} nnz={g.nnz} tasks={len(p.tasks)}", flush=True)
-    got, t = run_gpu(gpu_ctx, p, H)
+    got, t = run_gpu(gpu_ctx, p, H, flags=sched)
     ref32, ref64 = oracle_pair(p, g, H)
     check(got, ref32)
     check(got, ref64)
@@ -90,12 +105,12 @@ def test_small_config_candidates(gpu_ctx, cfg, which):
 
 
 @pytest.mark.parametrize("S", [1, 2, 3, 7, 32, 1000])
-def test_small_rmat_segment_sizes(gpu_ctx, S):
+def test_small_rmat_segment_sizes(gpu_ctx, sched, S):
     """Heavy splitting (S=1) through no splitting (S=1000) on a skewed graph."""
     g = workloads.small(4, seed=11)
     H = synth.features(g.n, 128, 7)
     p = problem(g, UNIT_COSTS, S)
-    got, _ = run_gpu(gpu_ctx, p, H)
+    got, _ = run_gpu(gpu_ctx, p, H, flags=sched)
     ref32, ref64 = oracle_pair(p, g, H)
     check(got, ref32)
     check(got, ref64)
@@ -168,9 +183,20 @@ def split_rows(p):
     return np.unique(np.concatenate([rs[first], re[last] - 1]))
 
 
+def tasks_per_row(p):
+    """Number of tasks that touch each reordered row."""
+    t = np.asarray(p.tasks, np.int64).reshape(-1, 4)
+    cnt = np.zeros(p.n + 1, np.int64)
+    np.add.at(cnt, t[:, 0], 1)
+    np.add.at(cnt, t[:, 1], -1)
+    return np.cumsum(cnt)[:-1]
+
+
 @pytest.mark.parametrize("cfg", [3, 4, 5])
-def test_full_config_properties(gpu_ctx, cfg):
+@pytest.mark.parametrize("per_task", [False, True], ids=["auto", "per_task"])
+def test_full_config_properties(gpu_ctx, cfg, per_task):
     torch = torch_mod()
+    flags = capi.PER_TASK if per_task else 0
     g = workloads.graph(cfg)
     K = workloads.FEATURE_DIM[cfg]
     S = workloads.candidate_s(g.nnz, 256)[0]
@@ -179,29 +205,39 @@ def test_full_config_properties(gpu_ctx, cfg):
     d_rp, d_ci, d_v, d_o = dev(p.row_ptr), dev(p.col_idx), dev(p.val), dev(p.origin)
     d_t = dev(np.ascontiguousarray(p.tasks, np.int32).reshape(-1))
     C = torch.full((g.n, K), float("nan"), dtype=torch.float32, device="cuda")
-    # All-ones features: every row with edges averages unit values to exactly 1.
+    # All-ones features: rows that no task splits average to exactly 1 (or
+    # 0 without edges).  A split row sums per-segment means in float, as the
+    # reference's atomics do; on hub rows with thousands of equal segment
+    # means that drifts from 1 by more than the parity tolerance, in the
+    # reference as much as here, so split rows are held to the rounding
+    # bound (touching tasks + 1) * 2^-23, which the reference-order oracle
+    # must meet too.
     ones = torch.ones((g.n, K), dtype=torch.float32, device="cuda")
-    gpu_ctx.spmm(d_rp, d_ci, d_v, d_o, g.n, g.nnz, ones, g.n, K, d_t, len(p.tasks), C)
+    gpu_ctx.spmm(d_rp, d_ci, d_v, d_o, g.n, g.nnz, ones, g.n, K, d_t, len(p.tasks), C,
+                 flags=flags)
     del ones
-    # Every column equals the K=1 aggregation of ones.  Split rows sum their
-    # per-segment means in float (as the reference's atomics do), which can
-    # drift from 1 by more than the tolerance on hub rows, so the check is
-    # against the reference-order oracle; unsplit rows are exactly 1 or 0.
-    ref1 = oracle.spmm_mean_f32(p.row_ptr, p.col_idx, p.val, p.origin,
-                                np.ones((g.n, 1), np.float32), p.tasks)
     got = C.cpu().numpy()
-    np.testing.assert_allclose(got, np.broadcast_to(ref1, got.shape), rtol=RTOL, atol=ATOL)
+    touch = np.zeros(g.n, np.int64)
+    touch[p.origin] = tasks_per_row(p)
     split = np.zeros(g.n, bool)
     split[p.origin[split_rows(p)]] = True
     deg = np.diff(g.row_ptr)
     exact = np.where(deg > 0, 1.0, 0.0).astype(np.float32)
     assert np.array_equal(got[~split], np.broadcast_to(exact[~split, None], got[~split].shape))
+    bound = (touch[split] + 1) * 2.0**-23
+    assert np.all(np.abs(got[split] - 1.0) <= bound[:, None])
+    ref1 = oracle.spmm_mean_f32(p.row_ptr, p.col_idx, p.val, p.origin,
+                                np.ones((g.n, 1), np.float32), p.tasks)
+    assert np.all(np.abs(ref1[split, 0] - 1.0) <= bound)
+    if per_task:
+        np.testing.assert_allclose(got, np.broadcast_to(ref1, got.shape), rtol=RTOL, atol=ATOL)
     del got
     # Seeded U[-1,1) features: sampled rows against the fp64 closed form.
     H = torch.empty((g.n, K), dtype=torch.float32, device="cuda")
     gpu_ctx.fill_features(H, g.n, K, workloads.FEATURE_SEED)
     C.fill_(float("nan"))
-    t = gpu_ctx.spmm(d_rp, d_ci, d_v, d_o, g.n, g.nnz, H, g.n, K, d_t, len(p.tasks), C)
+    t = gpu_ctx.spmm(d_rp, d_ci, d_v, d_o, g.n, g.nnz, H, g.n, K, d_t, len(p.tasks), C,
+                     flags=flags)
     assert not torch.isnan(C).any().item()
     H_host = synth.features(g.n, K, workloads.FEATURE_SEED)
     sampled_rows_check(g, C, H_host, np.random.default_rng(cfg))
@@ -209,12 +245,18 @@ def test_full_config_properties(gpu_ctx, cfg):
 
 
 # ------------------------------------------------------------------ edge cases
-@pytest.mark.parametrize("K", [1, 2, 3, 4, 6, 12, 20, 36, 100, 128, 256, 260, 600, 1000, 1024])
-def test_feature_widths(gpu_ctx, K):
+@pytest.mark.parametrize("K", [1, 2, 3, 4, 6, 12, 20, 36, 64, 100, 128, 192, 256, 260, 512, 600,
+                               1000, 1024])
+@pytest.mark.parametrize("m,sl", [(1, 1), (8, 2), (8, 4), (4, 8)])
+def test_feature_widths(gpu_ctx, K, m, sl):
     g = workloads.small(4, seed=3)
     H = synth.features(g.n, K, 5)
     p = problem(g, SKEWED_COSTS, 8)
-    got, _ = run_gpu(gpu_ctx, p, H)
+    gpu_ctx.set_schedule(m, sl)
+    try:
+        got, _ = run_gpu(gpu_ctx, p, H)
+    finally:
+        gpu_ctx.set_schedule(0, 0)
     ref32, ref64 = oracle_pair(p, g, H)
     check(got, ref32)
     check(got, ref64)
@@ -244,7 +286,7 @@ def test_large_k_entry_rejects_small_k(gpu_ctx):
     assert e.value.status == capi.INVALID_ARG
 
 
-def test_hub_row_and_empty_rows(gpu_ctx, rng):
+def test_hub_row_and_empty_rows(gpu_ctx, sched, rng):
     """One row of degree 5,000 among degree-0 and degree-1 rows, tiny S."""
     n = 6000
     deg = np.zeros(n, np.int64)
@@ -257,7 +299,7 @@ def test_hub_row_and_empty_rows(gpu_ctx, rng):
     H = synth.features(n, 64, 1)
     for S in (1, 2, 3, 64, 4999, 5000, 6000):
         p = problem(g, UNIT_COSTS, S)
-        got, _ = run_gpu(gpu_ctx, p, H)
+        got, _ = run_gpu(gpu_ctx, p, H, flags=sched)
         ref32, ref64 = oracle_pair(p, g, H)
         check(got, ref32)
         check(got, ref64)
@@ -272,7 +314,7 @@ def test_all_rows_empty(gpu_ctx):
     assert np.array_equal(got, np.zeros((n, 32), np.float32))
 
 
-def test_duplicate_columns_and_values(gpu_ctx, rng):
+def test_duplicate_columns_and_values(gpu_ctx, sched, rng):
     """Repeated columns inside a row and non-unit values."""
     n = 3000
     deg = rng.integers(0, 40, n)
@@ -283,7 +325,7 @@ def test_duplicate_columns_and_values(gpu_ctx, rng):
     H = synth.features(n, 64, 3)
     for S in (2, 5, 17):
         p = problem(g, SKEWED_COSTS, S)
-        got, _ = run_gpu(gpu_ctx, p, H)
+        got, _ = run_gpu(gpu_ctx, p, H, flags=sched)
         ref32, ref64 = oracle_pair(p, g, H)
         check(got, ref32)
         check(got, ref64)
