@@ -29,7 +29,7 @@ sys.path.insert(0, os.path.join(ROOT, "cwlb-spmm_amd"))
 METRIC = "SpMM GFLOP/s (2·nnz·K/t) + achieved HBM GB/s vs peak, FP32 mean agg"
 HBM_PEAK_GBS = 8000.0
 COST_FILE = os.path.join(ROOT, "cwlb-spmm_amd", "resources", "spmm_costs_gfx950.txt")
-PMC_SUMMARY = os.path.join(ROOT, "profiles", "spmm_mean_tasks_rmat22_k128_pmc.txt")
+PMC_SUMMARY = os.path.join(ROOT, "profiles", "spmm_mean_runs_rmat22_k128_pmc.txt")
 
 
 def log(msg):
