@@ -1,13 +1,171 @@
-// Degree reordering on the GPU (reference main.cpp:197-278, produced there
-// on the host with oneDPL).  Placeholder until the device sort lands.
+// Degree reordering on the GPU: the permutation, offsets and row copies of
+// the reference's host reordering (main.cpp:197-278), computed from device
+// arrays.
+//
+//   1. degree_keys: deg[i] = row_ptr[i+1] - row_ptr[i] as the sort key,
+//      with the CSR checks of the host form (offsets inside [0, nnz],
+//      non-decreasing) and the maximum degree;
+//   2. a stable LSD radix sort of (deg, i) pairs over the bits the maximum
+//      degree needs (rocPRIM): equal degrees keep ascending original ids, so
+//      the order is the reference comparator's (degree, id) order;
+//   3. row_ptr_out = 0 followed by the inclusive scan of the sorted degrees;
+//   4. gather_rows: each reordered row copies its entries from the original
+//      row, a lane per short row, the whole wave on rows longer than 16.
+// The call synchronises on the context's stream.
+#include <rocprim/device/device_radix_sort.hpp>
+#include <rocprim/device/device_scan.hpp>
+#include <rocprim/iterator/counting_iterator.hpp>
+
 #include "internal.h"
 
 namespace cwlb {
+namespace {
 
-cwlb_status launch_reorder(cwlb_ctx*, int32_t, int64_t, const int32_t*, const int32_t*,
-                           const float*, int32_t*, int32_t*, int32_t*, float*)
+constexpr int kBlock = 256;
+constexpr int kLaneRowMax = 16;
+
+// status bit 0: an offset outside [0, nnz] or a decreasing pair.
+__global__ void __launch_bounds__(kBlock)
+degree_keys(const int* __restrict__ rp, int n, long long nnz, unsigned* __restrict__ deg,
+            int* __restrict__ status, unsigned* __restrict__ max_deg)
 {
-    return fail(CWLB_UNSUPPORTED, "cwlb_reorder_by_degree_device: not available in this build");
+    const int i = blockIdx.x * kBlock + threadIdx.x;
+    unsigned d = 0;
+    if (i < n) {
+        const int a = rp[i];
+        const int b = rp[i + 1];
+        if (a < 0 || b < a || static_cast<long long>(b) > nnz) {
+            atomicOr(status, 1);
+        } else {
+            d = static_cast<unsigned>(b - a);
+        }
+        deg[i] = d;
+    }
+    // Wave maximum, then one atomic per wave.
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) d = max(d, static_cast<unsigned>(__shfl_xor(static_cast<int>(d), off)));
+    if ((threadIdx.x & 63) == 0 && d > 0) atomicMax(max_deg, d);
+}
+
+__global__ void __launch_bounds__(kBlock)
+gather_rows(const int* __restrict__ rp, const int* __restrict__ ci, const float* __restrict__ val,
+            const int* __restrict__ origin, const int* __restrict__ rp_out, int n,
+            int* __restrict__ ci_out, float* __restrict__ val_out)
+{
+    const int lane = threadIdx.x & 63;
+    const int r = blockIdx.x * kBlock + threadIdx.x;
+    int src = 0, dst = 0, len = 0;
+    if (r < n) {
+        const int o = origin[r];
+        src = rp[o];
+        dst = rp_out[r];
+        len = rp_out[r + 1] - dst;
+    }
+    if (len <= kLaneRowMax) {
+        for (int j = 0; j < len; ++j) {
+            ci_out[dst + j] = ci[src + j];
+            val_out[dst + j] = val[src + j];
+        }
+    }
+    unsigned long long m = __ballot(len > kLaneRowMax);
+    while (m) {
+        const int l = __ffsll(static_cast<long long>(m)) - 1;
+        m &= m - 1;
+        const int s = __shfl(src, l);
+        const int d = __shfl(dst, l);
+        const int c = __shfl(len, l);
+        for (int j = lane; j < c; j += 64) {
+            ci_out[d + j] = ci[s + j];
+            val_out[d + j] = val[s + j];
+        }
+    }
+}
+
+__global__ void set_first_zero(int* __restrict__ p) { p[0] = 0; }
+
+struct DevMem {
+    void* p = nullptr;
+    ~DevMem()
+    {
+        if (p) (void)hipFree(p);
+    }
+    hipError_t alloc(size_t bytes) { return hipMalloc(&p, bytes ? bytes : 1); }
+};
+
+unsigned bits_for(unsigned v)
+{
+    unsigned b = 0;
+    while (b < 32 && (v >> b) != 0) ++b;
+    return b;
+}
+
+}  // namespace
+
+cwlb_status launch_reorder(cwlb_ctx* ctx, int32_t n, int64_t nnz, const int32_t* rp,
+                           const int32_t* ci, const float* val, int32_t* origin, int32_t* rp_out,
+                           int32_t* ci_out, float* val_out)
+{
+    hipStream_t st = ctx->stream;
+    if (n == 0) {
+        if (!rp_out) return fail(CWLB_INVALID_ARG, "reorder: null row_ptr_out");
+        hipLaunchKernelGGL(set_first_zero, dim3(1), dim3(1), 0, st, rp_out);
+        CWLB_HIP_TRY(hipGetLastError());
+        CWLB_HIP_TRY(hipStreamSynchronize(st));
+        return CWLB_OK;
+    }
+    if (!rp || !origin || !rp_out || (nnz > 0 && (!ci || !val || !ci_out || !val_out)))
+        return fail(CWLB_INVALID_ARG, "reorder: null device pointer");
+
+    const size_t un = static_cast<size_t>(n);
+    DevMem keys, keys_sorted, flags;
+    CWLB_HIP_TRY(keys.alloc(sizeof(unsigned) * un));
+    CWLB_HIP_TRY(keys_sorted.alloc(sizeof(unsigned) * un));
+    CWLB_HIP_TRY(flags.alloc(2 * sizeof(int)));
+    auto* d_keys = static_cast<unsigned*>(keys.p);
+    auto* d_sorted = static_cast<unsigned*>(keys_sorted.p);
+    auto* d_status = static_cast<int*>(flags.p);
+    auto* d_max = reinterpret_cast<unsigned*>(d_status + 1);
+    CWLB_HIP_TRY(hipMemsetAsync(d_status, 0, 2 * sizeof(int), st));
+    const unsigned grid = static_cast<unsigned>((un + kBlock - 1) / kBlock);
+    hipLaunchKernelGGL(degree_keys, dim3(grid), dim3(kBlock), 0, st, rp, n,
+                       static_cast<long long>(nnz), d_keys, d_status, d_max);
+    CWLB_HIP_TRY(hipGetLastError());
+    int host_flags[2] = {0, 0};
+    int ends[2] = {0, 0};
+    CWLB_HIP_TRY(hipMemcpyAsync(host_flags, d_status, sizeof host_flags, hipMemcpyDeviceToHost, st));
+    CWLB_HIP_TRY(hipMemcpyAsync(&ends[0], rp, sizeof(int), hipMemcpyDeviceToHost, st));
+    CWLB_HIP_TRY(hipMemcpyAsync(&ends[1], rp + n, sizeof(int), hipMemcpyDeviceToHost, st));
+    CWLB_HIP_TRY(hipStreamSynchronize(st));
+    if (host_flags[0] & 1)
+        return fail(CWLB_INVALID_ARG, "cwlb_reorder_by_degree_device: row_ptr not a CSR offset array");
+    if (static_cast<int64_t>(ends[1]) - ends[0] != nnz)
+        return fail(CWLB_RUNTIME_ERROR,
+                    "DPL CPU degree reordering produced an inconsistent NNZ count.");
+    const unsigned end_bit = std::max(1u, bits_for(static_cast<unsigned>(host_flags[1])));
+
+    rocprim::counting_iterator<int> ids(0);
+    size_t sort_bytes = 0, scan_bytes = 0;
+    CWLB_HIP_TRY(rocprim::radix_sort_pairs(nullptr, sort_bytes, d_keys, d_sorted, ids, origin, un,
+                                           0u, end_bit, st));
+    CWLB_HIP_TRY(rocprim::inclusive_scan(nullptr, scan_bytes, d_sorted, rp_out + 1, un,
+                                         rocprim::plus<unsigned>(), st));
+    DevMem temp;
+    CWLB_HIP_TRY(temp.alloc(std::max(sort_bytes, scan_bytes)));
+    size_t bytes = sort_bytes;
+    CWLB_HIP_TRY(rocprim::radix_sort_pairs(temp.p, bytes, d_keys, d_sorted, ids, origin, un, 0u,
+                                           end_bit, st));
+    bytes = scan_bytes;
+    CWLB_HIP_TRY(rocprim::inclusive_scan(temp.p, bytes, d_sorted, rp_out + 1, un,
+                                         rocprim::plus<unsigned>(), st));
+    hipLaunchKernelGGL(set_first_zero, dim3(1), dim3(1), 0, st, rp_out);
+    CWLB_HIP_TRY(hipGetLastError());
+    if (nnz > 0) {
+        hipLaunchKernelGGL(gather_rows, dim3(grid), dim3(kBlock), 0, st, rp, ci, val, origin,
+                           rp_out, n, ci_out, val_out);
+        CWLB_HIP_TRY(hipGetLastError());
+    }
+    CWLB_HIP_TRY(hipStreamSynchronize(st));
+    return CWLB_OK;
 }
 
 }  // namespace cwlb

@@ -1,0 +1,370 @@
+"""The C++17 drop-in layer (include/config.h, Matrix.h, utils.h, data.h,
+cwlb_driver.h) and the cwlb-spmm / costWrite executables, on the CPU.
+
+The layer's functions run inside tests/cxx/bin/dropin_probe; their outputs
+are compared with the oracle (the reference's algorithm restated in C), the
+reference's own functions where oracle/_ref builds, numpy's MT19937 and
+hand-derived known answers.
+"""
+import os
+import subprocess
+
+import numpy as np
+import pytest
+
+import oracle
+from conftest import SKEWED_COSTS, UNIT_COSTS
+from cwlb_amd import workloads
+from dropin_util import (BIN, ProbeError, probe, read_csr, read_order, write_csr, write_f32,
+                         write_order)
+
+REF = oracle.ref()
+
+
+# ------------------------------------------------------------------ reorder
+@pytest.mark.parametrize("cfg", [1, 2, 3, 4, 5])
+def test_reorder_cpu_matches_oracle(tmp_path, cfg):
+    g = workloads.small(cfg)
+    write_csr(tmp_path / "in", g.row_ptr, g.col_idx, g.val)
+    probe("reorder-cpu", tmp_path / "in", tmp_path / "out")
+    got = read_order(tmp_path / "out")
+    exp = oracle.reorder_by_degree(g.row_ptr, g.col_idx, g.val)
+    for a, b in zip(got, exp):
+        assert np.array_equal(a, b)
+    # closed form: a stable argsort of the degrees
+    assert np.array_equal(got[0], np.argsort(np.diff(g.row_ptr), kind="stable"))
+
+
+def test_reorder_cpu_edge_cases(tmp_path):
+    # fewer than two offsets: empty result
+    write_csr(tmp_path / "in", [0], [], [])
+    probe("reorder-cpu", tmp_path / "in", tmp_path / "out")
+    assert all(len(a) == 0 for a in read_order(tmp_path / "out")[:1])
+    # offsets disagreeing with the entry count (main.cpp:273-276)
+    write_csr(tmp_path / "bad2", [0, 1, 5], [0, 1], [1, 1])
+    with pytest.raises(ProbeError) as e:
+        probe("reorder-cpu", tmp_path / "bad2", tmp_path / "out")
+    assert e.value.kind == "runtime_error"
+    assert "inconsistent NNZ" in e.value.msg
+
+
+# ---------------------------------------------------------------- partition
+APPENDIX_A = [
+    ([1, 1, 2, 10], [(0, 2, 0, 0), (2, 3, 0, 0), (3, 4, 0, 4), (3, 4, 4, 8), (3, 4, 8, 0)]),
+    ([1, 10], [(0, 2, 0, 2), (1, 2, 2, 6), (1, 2, 6, 0)]),
+    ([6, 9], [(0, 1, 0, 4), (0, 2, 4, 1), (1, 2, 1, 5), (1, 2, 5, 0)]),
+    ([1, 8], [(0, 1, 0, 0), (1, 2, 0, 4), (1, 2, 4, 0)]),
+    ([0, 0, 3], [(0, 3, 0, 0)]),
+]
+
+
+def order_from_degrees(degs):
+    rp = np.concatenate([[0], np.cumsum(degs)]).astype(np.int32)
+    n = len(degs)
+    return np.arange(n, dtype=np.int32), rp, np.zeros(rp[-1], np.int32), np.ones(rp[-1], np.float32)
+
+
+def run_partition(tmp_path, order, costs, S):
+    write_order(tmp_path / "ord", *order)
+    probe("partition", tmp_path / "ord", *costs, S, tmp_path / "tasks")
+    raw = open(tmp_path / "tasks", "rb").read()
+    cap = float(np.frombuffer(raw[:8], np.float64)[0])
+    tasks = np.frombuffer(raw[8:], np.int32).reshape(-1, 4)
+    return cap, tasks
+
+
+@pytest.mark.parametrize("degs,expected", APPENDIX_A)
+def test_partition_known_answers(tmp_path, degs, expected):
+    cap, tasks = run_partition(tmp_path, order_from_degrees(degs), UNIT_COSTS, 4)
+    assert cap == 4.5
+    assert [tuple(t) for t in tasks] == expected
+
+
+@pytest.mark.parametrize("cfg", [1, 2, 4, 5])
+def test_partition_matches_oracle_and_reference(tmp_path, cfg):
+    g = workloads.small(cfg)
+    order = oracle.reorder_by_degree(g.row_ptr, g.col_idx, g.val)
+    for costs in (UNIT_COSTS, SKEWED_COSTS):
+        for S in workloads.candidate_s(g.nnz, 256) + [1, 3]:
+            cap, tasks = run_partition(tmp_path, order, costs, S)
+            assert cap == oracle.capacity_from_s(S, costs)
+            assert np.array_equal(tasks, oracle.partition(order[1], costs, cap))
+            if REF is not None:
+                assert np.array_equal(tasks, oracle.ref_partition(order[1], costs, cap))
+
+
+def test_partition_empty(tmp_path):
+    cap, tasks = run_partition(tmp_path, (np.zeros(0), np.zeros(1), np.zeros(0), np.zeros(0)),
+                               UNIT_COSTS, 4)
+    assert len(tasks) == 0
+
+
+# ------------------------------------------------------------------- loader
+def dataset_tree(tmp_path, name, text):
+    build = tmp_path / "build"
+    data = tmp_path / "resources" / "datasets"
+    build.mkdir(exist_ok=True)
+    data.mkdir(parents=True, exist_ok=True)
+    if text is not None:
+        (data / name).write_text(text)
+    return build
+
+
+def load(tmp_path, file_name, text, arg=None):
+    build = dataset_tree(tmp_path, file_name, text)
+    out = probe("load", build, arg if arg is not None else file_name)
+    lines = out.splitlines()
+    V, E = int(lines[0].split()[1]), int(lines[0].split()[3])
+    rp = [int(x) for x in lines[1].split()[1:]]
+    ci = [int(x) for x in lines[2].split()[1:]]
+    val = [float(x) for x in lines[3].split()[1:]]
+    return V, E, rp, ci, val
+
+
+def test_loader_readme_example(tmp_path):
+    """The three-row, four-nonzero example of README.md:176-181."""
+    for arg in ("tiny", "tiny.csr"):
+        V, E, rp, ci, val = load(tmp_path, "tiny.csr", "0,2,3,4\n1,2,0,1\n", arg)
+        assert (V, E, rp, ci, val) == (3, 4, [0, 2, 3, 4], [1, 2, 0, 1], [1.0] * 4)
+
+
+def test_loader_tolerates_empty_cells_and_crlf(tmp_path):
+    V, E, rp, ci, _ = load(tmp_path, "g.csr", "0,1,,3\r\n2, 0,1\r\n")
+    assert (V, E, rp, ci) == (2, 3, [0, 1, 3], [2, 0, 1])
+
+
+def test_loader_empty_rows(tmp_path):
+    V, E, rp, ci, _ = load(tmp_path, "g.csr", "0,0,0\n\n")
+    assert (V, E, rp, ci) == (2, 0, [0, 0, 0], [])
+
+
+@pytest.mark.parametrize("text,kind,msg", [
+    (None, "runtime_error", "Failed to open .csr file: ../resources/datasets/g.csr"),
+    ("", "runtime_error", "Failed to read the first line of .csr file"),
+    ("0,1\n", "runtime_error", "Failed to read the second line of .csr file"),
+    (",,\n\n", "runtime_error", ".csr file has an empty RowOffset"),
+    ("0,-1\n\n", "runtime_error", "RowOffset.back(), namely NNZ, is negative"),
+    ("0,2\n1\n", "runtime_error", "ColInd size does not match RowOffset.back()(NNZ): ColInd=1, NNZ=2"),
+    ("1,2\n0,1\n", "runtime_error", "RowOffset[0] must be 0, current value is 1"),
+    ("0,2,1,2\n0,1\n", "runtime_error", "RowOffset is not monotonically non-decreasing at index 2"),
+    ("0,3,1\n0\n", "runtime_error", "RowOffset contains a value larger than NNZ at index 1"),
+    ("0,2\n0,-4\n", "runtime_error", "ColInd contains a negative column index"),
+    ("0,x\n0\n", "invalid_argument", "stoi"),
+])
+def test_loader_errors(tmp_path, text, kind, msg):
+    with pytest.raises(ProbeError) as e:
+        load(tmp_path, "g.csr", text, "g")
+    assert e.value.kind == kind
+    assert msg in e.value.msg
+
+
+def test_loader_empty_name(tmp_path):
+    build = dataset_tree(tmp_path, "g.csr", None)
+    with pytest.raises(ProbeError) as e:
+        probe("load", build, "")
+    assert e.value.msg == "Dataset name is empty"
+
+
+# ----------------------------------------------------------------- features
+def test_deterministic_features_match_mt19937(tmp_path):
+    """std::mt19937(42) + uniform_real_distribution<float>(0, 1), against
+    numpy's independent MT19937 with the same integer seeding: one 32-bit
+    draw per value, value = float(draw) / 2^32."""
+    rows, cols = 37, 29
+    probe("features", rows, cols, tmp_path / "f")
+    got = np.fromfile(tmp_path / "f", np.float32).reshape(rows, cols)
+    bg = np.random.MT19937()
+    bg._legacy_seeding(42)
+    draws = bg.random_raw(rows * cols)
+    exp = (draws.astype(np.float32) / np.float32(2.0**32)).astype(np.float32)
+    exp[exp >= 1.0] = np.nextafter(np.float32(1), np.float32(0))
+    assert np.array_equal(got.reshape(-1), exp)
+    assert got.min() >= 0.0 and got.max() < 1.0
+
+
+# ------------------------------------------------------------------ dense2csr
+def test_dense_to_csr(tmp_path, rng):
+    n = 23
+    A = rng.normal(size=(n, n)).astype(np.float32)
+    A[rng.random((n, n)) < 0.7] = 0.0
+    A[3, 5] = np.nan  # NaN != 0 is stored, as in the reference
+    write_f32(tmp_path / "A", A)
+    probe("dense2csr", n, n, tmp_path / "A", tmp_path / "csr")
+    rp, ci, val = read_csr(tmp_path / "csr")
+    rows, cols = np.nonzero(A != 0)  # row-major order
+    assert np.array_equal(rp, np.concatenate([[0], np.cumsum(np.bincount(rows, minlength=n))]))
+    assert np.array_equal(ci, cols)
+    assert np.array_equal(val, A[rows, cols], equal_nan=True)
+    with pytest.raises(ProbeError) as e:
+        probe("dense2csr", 2, 3, tmp_path / "A", tmp_path / "csr")
+    assert e.value.kind == "invalid_argument" and "square" in e.value.msg
+
+
+# ---------------------------------------------------------------- validator
+def validate(tmp_path, A, B, D=None, tol=1e-4, csr_rows=None):
+    rows, cols = A.shape
+    n = rows if csr_rows is None else csr_rows
+    write_f32(tmp_path / "A", A)
+    write_f32(tmp_path / "B", B)
+    D = np.ones((3, cols), np.float32) if D is None else D
+    write_f32(tmp_path / "D", D)
+    write_csr(tmp_path / "csr", np.arange(n + 1), np.zeros(n), np.ones(n))
+    out = probe("validate", tmp_path / "A", tmp_path / "B", tmp_path / "csr", tmp_path / "D",
+                rows, cols, D.shape[0], tol)
+    return out.strip().splitlines()[-1] == "RESULT pass", out
+
+
+def test_validator_rules(tmp_path):
+    nan, inf = np.float32(np.nan), np.float32(np.inf)
+    A = np.array([[1.0, nan, inf, -inf]], np.float32)
+    ok, _ = validate(tmp_path, A, A.copy())
+    assert ok
+    ok, out = validate(tmp_path, A, np.array([[1.0, 0.0, inf, -inf]], np.float32))
+    assert not ok and "Mismatch #1" in out and "Result matrix position: (0, 1)" in out
+    ok, _ = validate(tmp_path, A, np.array([[1.0, nan, -inf, -inf]], np.float32))
+    assert not ok
+    # the tolerance is inclusive: |a - b| > tol is a mismatch
+    a = np.array([[0.5]], np.float32)
+    ok, _ = validate(tmp_path, a, a + np.float32(0.25), tol=0.25)
+    assert ok
+    ok, _ = validate(tmp_path, a, a + np.float32(0.25), tol=0.2)
+    assert not ok
+
+
+def test_validator_reports_at_most_ten(tmp_path):
+    A = np.zeros((4, 5), np.float32)
+    ok, out = validate(tmp_path, A, A + 1)
+    assert not ok
+    assert "showing 10 mismatched elements" in out and "Mismatch #10" in out
+    assert "Mismatch #11" not in out
+
+
+def test_validator_shape_errors(tmp_path):
+    A = np.zeros((2, 2), np.float32)
+    assert not validate(tmp_path, A, A, csr_rows=3)[0]
+    assert not validate(tmp_path, A, A, D=np.zeros((0, 2), np.float32))[0]
+    ok, out = validate(tmp_path, A, A, tol=-1.0)
+    assert not ok
+
+
+# ------------------------------------------------------------- S selection
+def test_selection_matches_oracle():
+    for nnz in (0, 1, 99_999, 100_000, 65_245_138, 10**9):
+        out = probe("select", nnz, 2, 256, 64).splitlines()
+        w = [int(x) for x in out[0].split()[1:]]
+        assert w == oracle.recommended_candidate_w(nnz)
+        assert int(out[1].split()[1]) == oracle.wave_based_s(nnz, 2, 256, 64)
+    assert probe("select", 5, 0, 256, 64).splitlines()[1] == "s 1"
+    with pytest.raises(ProbeError) as e:
+        probe("select", 5, 2, 0, 64)
+    assert e.value.kind == "invalid_argument"
+
+
+def test_search_grids_readme_examples():
+    """README.md:342-345, 369-376 and the grid rules of main.cpp:130-167."""
+    assert probe("search", 2, 30, "step", 2).split()[1:] == [str(x) for x in range(2, 31, 2)]
+    assert probe("search", 10, 20, "step", 4).split()[1:] == ["10", "14", "18", "20"]
+    for lo, hi, c in ((1, 100, 6), (5, 7, 6), (3, 3, 1), (10, 20, 1)):
+        got = [int(x) for x in probe("search", lo, hi, "count", c).split()[1:]]
+        assert got == oracle.candidate_search_by_count(lo, hi, c)
+    with pytest.raises(ProbeError) as e:
+        probe("search", 1, 10**6, "step", 1)
+    assert "exceeds 10000 points" in e.value.msg
+
+
+def test_bounds_and_positive_argument():
+    assert probe("bounds", 32, 63, 125, 0).split()[1:] == ["1", "63"]
+    assert probe("bounds", 32, 63, 125, 1).split()[1:] == ["32", "125"]
+    assert probe("bounds", 32, 63, 125, 2).split()[1:] == ["63", "187"]
+    with pytest.raises(ProbeError):
+        probe("bounds", 32, 10, 125, 1)
+    assert probe("posarg", "12").split()[1] == "12"
+    for bad in ("0", "-3", "3x", "x"):
+        with pytest.raises(ProbeError) as e:
+            probe("posarg", bad)
+        assert e.value.kind == "invalid_argument"
+
+
+# ---------------------------------------------------------------- cost file
+def test_cost_file_roundtrip(tmp_path):
+    p = tmp_path / "sub" / "costs.txt"
+    c4 = (0.004519, 0.015617, 0.010667, 0.540499)
+    assert probe("costs-save", p, 0, 6, *c4).split()[1] == "1"
+    assert p.read_text() == oracle.format_costs(c4, 6)
+    if REF is not None:
+        assert p.read_text() == oracle.ref_format_costs(c4, 6)
+    out = probe("costs-read", p).split()
+    assert out[1] == "1" and [float(x) for x in out[2:6]] == list(c4) and out[7] == "7"
+    assert probe("costs-save", p, 1, 3, 1, 2, 3, 4).split()[1] == "1"
+    assert p.read_text().endswith("1.000\n2.000\n3.000\n4.000\n")
+    (tmp_path / "file").write_text("x")
+    assert probe("costs-save", tmp_path / "file" / "c.txt", 0, 6, *c4).split()[1] == "0"
+    assert probe("costs-read", tmp_path / "missing").split()[1] == "0"
+    (tmp_path / "short").write_text("1\n2\n3\n")
+    assert probe("costs-read", tmp_path / "short").split()[1] == "0"
+
+
+def test_device_construction_without_gpu_fails_cleanly():
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is visible")
+    with pytest.raises(ProbeError) as e:
+        probe("device")
+    assert e.value.kind == "runtime_error"
+
+
+# ------------------------------------------------------------- executables
+def run_exe(name, *args, cwd=None, stdin=""):
+    return subprocess.run([os.path.join(BIN, name), *map(str, args)], capture_output=True,
+                          text=True, cwd=cwd, input=stdin, timeout=300)
+
+
+@pytest.mark.parametrize("args,msg", [
+    ([], "Usage:"),
+    (["g"], "Usage:"),
+    (["g", "32", "1", "2", "3", "4"], "Usage:"),
+    (["g", "0", "8"], "K and the hyperparameter must be positive."),
+    (["g", "32", "0"], "K and the hyperparameter must be positive."),
+    (["g", "32", "--S", "-1"], "K and the hyperparameter must be positive."),
+    (["g", "32", "5", "6"], "The five-argument form must use --S."),
+    (["g", "32", "--candidate-search", "0"], "Search count/step must be a positive integer."),
+    (["g", "32", "--candidate-search", "--step", "x"], "stoi"),
+    (["g", "32", "--candidate-search", "--stp", "3"],
+     "Use --candidate-search [count] or --candidate-search --step step."),
+    (["g", "32", "4", "2", "1"], "S_begin must not be greater than S_max."),
+    (["g", "32", "1", "2", "0"], "S_begin, S_max and S_step must be positive."),
+    (["g", "abc", "8"], "stoi"),
+])
+def test_cwlb_spmm_argument_errors(tmp_path, args, msg):
+    r = run_exe("cwlb-spmm", *args, cwd=tmp_path)
+    assert r.returncode == 1
+    assert msg in r.stderr
+
+
+def test_cwlb_spmm_missing_dataset(tmp_path):
+    build = dataset_tree(tmp_path, "g.csr", None)
+    r = run_exe("cwlb-spmm", "nothere", 32, "--S", 8, cwd=build)
+    assert r.returncode == 1
+    assert "Failed to open .csr file: ../resources/datasets/nothere.csr" in r.stderr
+
+
+def test_cwlb_spmm_without_gpu_fails_after_loading(tmp_path):
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is visible")
+    build = dataset_tree(tmp_path, "g.csr", "0,2,3,4\n1,2,0,1\n")
+    r = run_exe("cwlb-spmm", "g", 32, "--S", 8, cwd=build)
+    assert r.returncode == 1 and r.stderr.strip()
+
+
+@pytest.mark.parametrize("args,msg", [
+    (["1"], "Usage:"),
+    (["1", "2", "3", "4"], "Usage:"),
+    (["128", "0", "1", "1", "1"], "All microbenchmark parameters must be positive."),
+    (["128", "5", "1", "-1", "1"], "All microbenchmark parameters must be positive."),
+    (["x", "5", "1", "1", "1"], "stoi"),
+])
+def test_cost_write_argument_errors(tmp_path, args, msg):
+    r = run_exe("costWrite", *args, cwd=tmp_path)
+    assert r.returncode == 1
+    assert msg in r.stderr

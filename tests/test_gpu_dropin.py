@@ -1,0 +1,307 @@
+"""GPU tests of the device degree reordering, the calibration, the C++17
+drop-in layer (through tests/cxx/bin/dropin_probe) and the cwlb-spmm /
+costWrite executables.
+
+Parity bar: the reordering is bit-exact with the oracle (the reference's
+(degree, id) order); aggregated features within 1e-5 relative + 1e-6
+absolute of the reference-order oracle and of the fp64 closed form.
+"""
+import os
+import subprocess
+
+import numpy as np
+import pytest
+
+import oracle
+from conftest import SKEWED_COSTS, UNIT_COSTS
+from cwlb_amd import capi, synth, workloads
+from dropin_util import (BIN, ProbeError, probe, read_order, write_csr, write_f32, write_order,
+                         write_tasks)
+
+pytestmark = pytest.mark.gpu
+
+RTOL, ATOL = 1e-5, 1e-6
+
+
+def dev(a):
+    import torch
+    a = np.ascontiguousarray(a)
+    if a.size == 0:
+        a = np.zeros(1, a.dtype)
+    return torch.from_numpy(a).cuda()
+
+
+def reorder_on_device(ctx, rp, ci, val):
+    import torch
+    n = len(rp) - 1
+    nnz = len(ci)
+    origin = torch.full((max(n, 1),), -7, dtype=torch.int32, device="cuda")
+    rp_out = torch.full((n + 1,), -7, dtype=torch.int32, device="cuda")
+    ci_out = torch.full((max(nnz, 1),), -7, dtype=torch.int32, device="cuda")
+    v_out = torch.full((max(nnz, 1),), -7.0, dtype=torch.float32, device="cuda")
+    ctx.reorder_device(n, nnz, dev(rp), dev(ci), dev(val), origin, rp_out, ci_out, v_out)
+    return (origin.cpu().numpy()[:n], rp_out.cpu().numpy(), ci_out.cpu().numpy()[:nnz],
+            v_out.cpu().numpy()[:nnz])
+
+
+def assert_same_order(got, exp):
+    for a, b in zip(got, exp):
+        assert np.array_equal(a, b)
+
+
+# ------------------------------------------------------ device reordering
+@pytest.mark.parametrize("cfg", [1, 2, 3, 4, 5])
+def test_device_reorder_small(gpu_ctx, cfg):
+    g = workloads.small(cfg)
+    got = reorder_on_device(gpu_ctx, g.row_ptr, g.col_idx, g.val)
+    assert_same_order(got, oracle.reorder_by_degree(g.row_ptr, g.col_idx, g.val))
+
+
+@pytest.mark.parametrize("cfg", [4, 5])
+def test_device_reorder_full(gpu_ctx, cfg):
+    """Full-size R-MAT (max degree ~1e5) and mesh (N = 16M): bit-exact with
+    the host reordering, which the CPU tests pin to the oracle."""
+    g = workloads.graph(cfg)
+    print(f"cfg={cfg} n={g.n} nnz={g.nnz}", flush=True)
+    got = reorder_on_device(gpu_ctx, g.row_ptr, g.col_idx, g.val)
+    exp = capi.reorder_by_degree(g.row_ptr, g.col_idx, g.val)
+    assert_same_order(got, exp)
+    assert np.array_equal(got[0], np.argsort(np.diff(g.row_ptr), kind="stable"))
+
+
+def test_device_reorder_edge_cases(gpu_ctx, rng):
+    # no rows
+    got = reorder_on_device(gpu_ctx, np.zeros(1, np.int32), np.zeros(0, np.int32),
+                            np.zeros(0, np.float32))
+    assert list(got[1]) == [0]
+    # all rows empty, then hub rows next to empty and short rows, values kept
+    for degs in (np.zeros(1000, np.int64), np.array([0, 3000, 1, 17, 16, 0, 64, 65, 3000, 2])):
+        rp = np.concatenate([[0], np.cumsum(degs)]).astype(np.int32)
+        ci = rng.integers(0, 50, rp[-1]).astype(np.int32)
+        val = rng.normal(size=rp[-1]).astype(np.float32)
+        got = reorder_on_device(gpu_ctx, rp, ci, val)
+        assert_same_order(got, oracle.reorder_by_degree(rp, ci, val))
+
+
+def test_device_reorder_rejects_bad_offsets(gpu_ctx):
+    ci = np.zeros(4, np.int32)
+    val = np.ones(4, np.float32)
+    with pytest.raises(capi.CwlbError) as e:
+        reorder_on_device(gpu_ctx, np.array([0, 3, 2, 4], np.int32), ci, val)
+    assert e.value.status == capi.INVALID_ARG
+    with pytest.raises(capi.CwlbError) as e:
+        reorder_on_device(gpu_ctx, np.array([0, 1, 2, 3], np.int32), ci, val)
+    assert e.value.status == capi.RUNTIME_ERROR
+
+
+# ------------------------------------------------------------- calibration
+def test_calibration_small(gpu_ctx):
+    c = gpu_ctx.calibrate(K=64, repeat=3, WI=8192, load_MB=16, atomic_writers=8)
+    vals = c.tuple4()
+    assert all(np.isfinite(vals)) and all(v > 0 for v in vals), vals
+    assert (c.K, c.WI, c.repeat, c.atomic_writers_per_addr) == (64, 8192, 3, 8)
+    with pytest.raises(capi.CwlbError) as e:
+        gpu_ctx.calibrate(K=0, repeat=3, WI=8192, load_MB=16, atomic_writers=8)
+    assert e.value.status == capi.INVALID_ARG
+    with pytest.raises(capi.CwlbError) as e:
+        gpu_ctx.calibrate(K=1 << 20, repeat=1, WI=64, load_MB=1, atomic_writers=1)
+    assert e.value.status == capi.RUNTIME_ERROR  # data_MB_for_load too small for K
+
+
+# ------------------------------------------------------- drop-in C++ layer
+def test_dropin_device_properties():
+    out = probe("device").split()
+    props = dict(zip(out[::2], out[1::2]))
+    assert props["wg"] == "1024" and props["wave"] == "64"
+    assert props["arch"].startswith("gfx950")
+    assert int(props["cu"]) > 0
+
+
+@pytest.mark.parametrize("cfg", [1, 4])
+def test_dropin_reorder_gpu(tmp_path, cfg):
+    g = workloads.small(cfg)
+    write_csr(tmp_path / "in", g.row_ptr, g.col_idx, g.val)
+    probe("reorder-gpu", tmp_path / "in", tmp_path / "out")
+    assert_same_order(read_order(tmp_path / "out"),
+                      oracle.reorder_by_degree(g.row_ptr, g.col_idx, g.val))
+
+
+def spmm_case(tmp_path, cfg, K, S, costs=SKEWED_COSTS, seed=None):
+    g = workloads.small(cfg, seed)
+    p = workloads.prepare(g, costs, S)
+    H = synth.features(g.n, K, 7)
+    write_order(tmp_path / "ord", p.origin, p.row_ptr, p.col_idx, p.val)
+    write_f32(tmp_path / "H", H)
+    write_tasks(tmp_path / "tasks", p.tasks)
+    return g, p, H
+
+
+def oracle_check(got, g, p, H):
+    ref32 = oracle.spmm_mean_f32(p.row_ptr, p.col_idx, p.val, p.origin, H, p.tasks)
+    ref64 = oracle.spmm_mean_f64(g.row_ptr, g.col_idx, g.val, H)
+    np.testing.assert_allclose(got, ref32, rtol=RTOL, atol=ATOL)
+    np.testing.assert_allclose(got, ref64, rtol=RTOL, atol=ATOL)
+
+
+@pytest.mark.parametrize("cfg,K,S", [(1, 32, 4), (2, 64, 16), (3, 600, 8), (4, 128, 32),
+                                     (5, 32, 2)])
+def test_dropin_spmm_kernel(tmp_path, cfg, K, S):
+    g, p, H = spmm_case(tmp_path, cfg, K, S)
+    out = probe("spmm", tmp_path / "ord", tmp_path / "H", g.n, K, tmp_path / "tasks",
+                tmp_path / "C").split()
+    assert float(out[1]) > 0 and out[3] == str(g.n) and out[5] == str(K)
+    got = np.fromfile(tmp_path / "C", np.float32).reshape(g.n, K)
+    oracle_check(got, g, p, H)
+
+
+def test_dropin_large_k(tmp_path):
+    g, p, H = spmm_case(tmp_path, 1, 1100, 5, UNIT_COSTS, seed=9)
+    with pytest.raises(ProbeError) as e:
+        probe("spmm", tmp_path / "ord", tmp_path / "H", g.n, 1100, tmp_path / "tasks",
+              tmp_path / "C")
+    assert e.value.kind == "invalid_argument"
+    assert "use spmmKernelLargeKFallback for larger K" in e.value.msg
+    probe("spmm-large", tmp_path / "ord", tmp_path / "H", g.n, 1100, tmp_path / "tasks",
+          tmp_path / "C")
+    got = np.fromfile(tmp_path / "C", np.float32).reshape(g.n, 1100)
+    oracle_check(got, g, p, H)
+    g, p, H = spmm_case(tmp_path, 1, 64, 5, UNIT_COSTS, seed=9)
+    with pytest.raises(ProbeError) as e:
+        probe("spmm-large", tmp_path / "ord", tmp_path / "H", g.n, 64, tmp_path / "tasks",
+              tmp_path / "C")
+    assert e.value.msg == "spmmKernelLargeKFallback requires K > device max work-group size."
+
+
+def test_dropin_degenerate_calls(tmp_path):
+    g, p, H = spmm_case(tmp_path, 1, 32, 4)
+    # no tasks: zero matrix, time 0 (parallelMatrix.cpp:101-104)
+    write_tasks(tmp_path / "none", np.zeros((0, 4), np.int32))
+    out = probe("spmm", tmp_path / "ord", tmp_path / "H", g.n, 32, tmp_path / "none",
+                tmp_path / "C").split()
+    assert float(out[1]) == 0.0
+    assert not np.fromfile(tmp_path / "C", np.float32).any()
+    # K == 0 (parallelMatrix.cpp:80-83)
+    out = probe("spmm", tmp_path / "ord", tmp_path / "H", g.n, 0, tmp_path / "tasks",
+                tmp_path / "C").split()
+    assert float(out[1]) == 0.0 and out[5] == "0"
+    # a column index outside H
+    ci = p.col_idx.copy()
+    ci[0] = g.n + 3
+    write_order(tmp_path / "bad", p.origin, p.row_ptr, ci, p.val)
+    with pytest.raises(ProbeError) as e:
+        probe("spmm", tmp_path / "bad", tmp_path / "H", g.n, 32, tmp_path / "tasks",
+              tmp_path / "C")
+    assert e.value.kind == "invalid_argument"
+
+
+def test_dropin_run_single_s(tmp_path):
+    g = workloads.small(4, seed=6)
+    K, S = 128, 16
+    order = capi.reorder_by_degree(g.row_ptr, g.col_idx, g.val)
+    H = synth.features(g.n, K, 11)
+    write_order(tmp_path / "ord", *order)
+    write_f32(tmp_path / "H", H)
+    out = probe("run-single-s", tmp_path / "ord", tmp_path / "H", g.n, K, *SKEWED_COSTS, S,
+                tmp_path / "C").split()
+    rec = dict(zip(out[::2], out[1::2]))
+    assert float(rec["average"]) > 0 and rec["samples"] == "50"
+    cap = capi.capacity_from_s(S, SKEWED_COSTS)
+    tasks = oracle.partition(order[1], SKEWED_COSTS, cap)
+    assert int(rec["tasks"]) == len(tasks)
+    got = np.fromfile(tmp_path / "C", np.float32).reshape(g.n, K)
+    ref32 = oracle.spmm_mean_f32(order[1], order[2], order[3], order[0], H, tasks)
+    np.testing.assert_allclose(got, ref32, rtol=RTOL, atol=ATOL)
+
+
+# ------------------------------------------------------------- executables
+def cli_tree(tmp_path, g, costs=SKEWED_COSTS):
+    build = tmp_path / "build"
+    data = tmp_path / "resources" / "datasets"
+    build.mkdir()
+    data.mkdir(parents=True)
+    text = ",".join(map(str, g.row_ptr)) + "\n" + ",".join(map(str, g.col_idx)) + "\n"
+    (data / "g.csr").write_text(text)
+    capi.save_costs(costs, tmp_path / "resources" / "spmm_costs.txt")
+    return build
+
+
+def run_exe(name, *args, cwd=None, stdin=""):
+    r = subprocess.run([os.path.join(BIN, name), *map(str, args)], capture_output=True, text=True,
+                       cwd=cwd, input=stdin, timeout=300)
+    print(r.stdout[-3000:], r.stderr[-2000:], flush=True)
+    return r
+
+
+def test_cli_single_s_and_wave(tmp_path):
+    g = workloads.small(4, seed=2)
+    build = cli_tree(tmp_path, g)
+    r = run_exe("cwlb-spmm", "g", 64, "--S", 8, cwd=build)
+    assert r.returncode == 0
+    lines = r.stdout.splitlines()
+    assert sum(ln.startswith("[Warm-up ") for ln in lines) == 20
+    assert sum(ln.startswith("[Iteration ") for ln in lines) == 50
+    assert f"V: {g.n}, E: {g.nnz}" in r.stdout
+    t = float([ln for ln in lines if ln.startswith("SpMM time: ")][0].split()[2])
+    assert t > 0
+    r = run_exe("cwlb-spmm", "g.csr", 64, 64, cwd=build)
+    assert r.returncode == 0 and "Dataset: g.csr" in r.stdout
+
+
+def test_cli_missing_cost_file(tmp_path):
+    g = workloads.small(1)
+    build = cli_tree(tmp_path, g)
+    os.remove(tmp_path / "resources" / "spmm_costs.txt")
+    r = run_exe("cwlb-spmm", "g", 32, "--S", 8, cwd=build)
+    assert r.returncode == 1
+    assert ("Cannot read microbenchmark cost file: ../resources/spmm_costs.txt. "
+            "Run ./costWrite first.") in r.stderr
+
+
+def test_cli_candidates_and_search(tmp_path):
+    g = workloads.small(2, seed=3)
+    build = cli_tree(tmp_path, g)
+    r = run_exe("cwlb-spmm", "g", 32, "--candidates", cwd=build)
+    assert r.returncode == 0
+    assert "=== Candidate summary (SpMM kernel time, us) ===" in r.stdout
+    assert "best_candidate=S" in r.stdout
+    assert not (tmp_path / "resources" / "results.txt").exists()
+    # declined search: nothing written
+    r = run_exe("cwlb-spmm", "g", 32, "--candidate-search", 3, cwd=build, stdin="maybe\nno\n")
+    assert r.returncode == 0
+    assert "Please enter yes or no." in r.stdout
+    assert "Search cancelled; results.txt unchanged." in r.stdout
+    assert not (tmp_path / "resources" / "results.txt").exists()
+    # EOF at the prompt is a cancellation too
+    r = run_exe("cwlb-spmm", "g", 32, "--candidate-search", cwd=build, stdin="")
+    assert r.returncode == 0 and "Search cancelled" in r.stdout
+    # confirmed search: both blocks appended
+    r = run_exe("cwlb-spmm", "g", 32, "--candidate-search", "--step", 5, cwd=build,
+                stdin=" YES \n")
+    assert r.returncode == 0
+    assert "final_best_S=" in r.stdout and "Results appended to ../resources/results.txt" in r.stdout
+    text = (tmp_path / "resources" / "results.txt").read_text().splitlines()
+    assert text[0] == "cwlb-spmm-candidates\tg\t32"
+    assert text[4] == "cwlb-spmm-candidate-search\tg\t32"
+    plan = [ln for ln in r.stdout.splitlines() if ln.startswith("[Search plan] S values:")][0]
+    assert len(text) == 5 + len(plan.split()[4:])
+
+
+def test_cli_range_sweep(tmp_path):
+    g = workloads.small(5)
+    build = cli_tree(tmp_path, g)
+    r = run_exe("cwlb-spmm", "g", 32, 2, 7, 2, cwd=build)
+    assert r.returncode == 0
+    text = (tmp_path / "resources" / "results.txt").read_text().splitlines()
+    assert text[0] == "cwlb-spmm\tg\t32"
+    assert [ln.split("\t")[0] for ln in text[1:]] == ["2", "4", "6"]
+    assert "best_S=" in r.stdout
+
+
+def test_cost_write_small(tmp_path):
+    build = tmp_path / "build"
+    build.mkdir()
+    r = run_exe("costWrite", 64, 3, 8192, 16, 8, cwd=build)
+    assert r.returncode == 0
+    assert "Saved cost parameters to: ../resources/spmm_costs.txt" in r.stdout
+    vals = [float(x) for x in (tmp_path / "resources" / "spmm_costs.txt").read_text().split()]
+    assert len(vals) == 4 and all(v > 0 for v in vals)
