@@ -197,7 +197,7 @@ int run(int argc, char** argv)
         std::cout << "time " << time << " rows " << C.rows() << " cols " << C.cols() << "\n";
         write_dense(argv[7], C);
     } else if (cmd == "run-single-s") {
-        need(9);
+        need(10);
         const CSR_Order o = read_order(argv[2]);
         const Defined::RowMajorMatrixXf H = read_dense(argv[3], std::stol(argv[4]), std::stol(argv[5]));
         const SpmmCostParams c = costs_from(argv + 6);
