@@ -55,6 +55,8 @@ def main():
     ap.add_argument("--s", type=int, default=0, help="fixed segment size (0 = best candidate)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-host-call", action="store_true",
+                    help="skip the one host-pointer call (inputs copied in, C copied out)")
     ap.add_argument("--costs", default=COST_FILE, help="cost file (four coefficients)")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="also run one device-to-device copy of this many MiB (a known-size "
@@ -134,6 +136,17 @@ def main():
     per_task_us = float(np.mean([t.total_us for t in pt]))
     log(f"S={S} T={T} ms/step={ms_per_step:.3f} main_us={main_us:.1f} zero_us={zero_us:.1f}")
 
+    # The host-pointer boundary (the drop-in spmmKernel's transfers): one
+    # call with inputs in host memory, copied in and out (pageable).
+    host_call_ms = None
+    if not args.no_host_call:
+        Hh = H.cpu().numpy()
+        t1 = time.perf_counter()
+        ctx.spmm_host(rp, ci, val, origin, Hh, tasks)
+        host_call_ms = (time.perf_counter() - t1) * 1e3
+        del Hh
+        log(f"host-pointer call {host_call_ms:.1f} ms (PCIe transfers included)")
+
     if args.copy_probe_mib:
         nb = args.copy_probe_mib << 20
         src = torch.ones(nb // 4, dtype=torch.float32, device="cuda")
@@ -195,6 +208,7 @@ def main():
                    "tasks": T, "costs": list(costs), "device": info.name.decode(),
                    "main_kernel_us": round(main_us, 2), "zero_pass_us": round(zero_us, 2),
                    "per_task_mode_us": round(per_task_us, 2),
+                   "host_pointer_call_ms": None if host_call_ms is None else round(host_call_ms, 1),
                    "algorithmic_bytes": b_alg},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
