@@ -151,6 +151,9 @@ cwlb_status cwlb_ctx_destroy(cwlb_ctx* ctx)
     for (auto& ev : ctx->ev)
         if (ev) (void)hipEventDestroy(ev);
     if (ctx->d_status) (void)hipFree(ctx->d_status);
+    for (void* p : {static_cast<void*>(ctx->d_run_keys), static_cast<void*>(ctx->d_run_keys_sorted),
+                    static_cast<void*>(ctx->d_run_order), ctx->d_sort_temp})
+        if (p) (void)hipFree(p);
     delete ctx;
     return CWLB_OK;
 }
@@ -194,6 +197,20 @@ cwlb_status cwlb_ctx_set_schedule(cwlb_ctx* ctx, int32_t tasks_per_wave, int32_t
         return fail(CWLB_INVALID_ARG, "feature_slices must be 0, 1, 2, 4 or 8");
     ctx->sched_tasks_per_wave = tasks_per_wave;
     ctx->sched_slices = feature_slices;
+    return CWLB_OK;
+}
+
+cwlb_status cwlb_ctx_set_locality(cwlb_ctx* ctx, int32_t run_order, int32_t xcd_blocks)
+{
+    if (!ctx) return fail(CWLB_INVALID_ARG, "null context");
+    if (run_order < 0 || run_order > 2)
+        return fail(CWLB_INVALID_ARG, "run_order must be 0 (automatic), 1 (task order) or 2 "
+                                      "(by output row)");
+    if (xcd_blocks < 0 || xcd_blocks > 2)
+        return fail(CWLB_INVALID_ARG, "xcd_blocks must be 0 (automatic), 1 (interleaved) or 2 "
+                                      "(contiguous)");
+    ctx->sched_order = run_order;
+    ctx->sched_xcd = xcd_blocks;
     return CWLB_OK;
 }
 

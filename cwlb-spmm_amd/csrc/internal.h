@@ -22,9 +22,21 @@ struct cwlb_ctx {
     // Device status word written by the kernels: bit 0 = a column index was
     // outside [0, h_rows), bit 1 = an origin entry was outside [0, n_rows).
     int* d_status = nullptr;
-    // Schedule overrides (0 = automatic): tasks per wave, feature slices.
+    // Schedule overrides (0 = automatic): tasks per wave, feature slices,
+    // run order (1 = task order, 2 = by output row id) and block placement
+    // over the XCDs (1 = interleaved, 2 = contiguous per XCD).
     int sched_tasks_per_wave = 0;
     int sched_slices = 0;
+    int sched_order = 0;
+    int sched_xcd = 0;
+    // Grow-only device buffers for the run order: keys, sorted keys, the
+    // order itself and the sort's temporary storage.
+    unsigned* d_run_keys = nullptr;
+    unsigned* d_run_keys_sorted = nullptr;
+    int* d_run_order = nullptr;
+    long long run_cap = 0;
+    void* d_sort_temp = nullptr;
+    size_t sort_temp_bytes = 0;
 };
 
 namespace cwlb {
@@ -74,6 +86,12 @@ struct SpmmArgs {
 // per_task runs one task per wave (no task-run fusion, no feature slices).
 cwlb_status launch_spmm_mean(cwlb_ctx* ctx, const SpmmArgs& a, bool zero_all, bool per_task,
                              bool record_events);
+
+// Computes into ctx->d_run_order a permutation of the n_runs runs (runs of
+// M tasks) sorted by the original id of each run's first row, on
+// ctx->stream; *order receives ctx->d_run_order.
+cwlb_status build_run_order(cwlb_ctx* ctx, const SpmmArgs& a, int M, long long n_runs,
+                            const int** order);
 
 cwlb_status launch_fill_features(cwlb_ctx* ctx, float* H, int64_t rows, int32_t K, uint64_t seed);
 

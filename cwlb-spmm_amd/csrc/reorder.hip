@@ -99,7 +99,72 @@ unsigned bits_for(unsigned v)
     return b;
 }
 
+// key[r] = original id of the first row of run r (runs of M tasks).
+__global__ void __launch_bounds__(kBlock)
+run_keys(const cwlb_task* __restrict__ tasks, long long n_tasks, int M, long long n_runs,
+         const int* __restrict__ origin, int n_rows, unsigned* __restrict__ keys)
+{
+    const long long r = static_cast<long long>(blockIdx.x) * kBlock + threadIdx.x;
+    if (r >= n_runs) return;
+    const long long t = r * M < n_tasks ? r * M : n_tasks - 1;
+    const int rs = min(max(tasks[t].row_start, 0), n_rows - 1);
+    keys[r] = static_cast<unsigned>(origin[rs]);
+}
+
+template <class T>
+cwlb_status grow(T** p, long long have, long long want)
+{
+    if (want <= have && *p) return CWLB_OK;
+    if (*p) CWLB_HIP_TRY(hipFree(*p));
+    *p = nullptr;
+    CWLB_HIP_TRY(hipMalloc(reinterpret_cast<void**>(p), sizeof(T) * static_cast<size_t>(want)));
+    return CWLB_OK;
+}
+
 }  // namespace
+
+cwlb_status build_run_order(cwlb_ctx* ctx, const SpmmArgs& a, int M, long long n_runs,
+                            const int** order)
+{
+    hipStream_t st = ctx->stream;
+    if (n_runs <= 0 || a.n_rows <= 0) {
+        *order = nullptr;
+        return CWLB_OK;
+    }
+    if (n_runs > ctx->run_cap) {
+        cwlb_status s = grow(&ctx->d_run_keys, 0, n_runs);
+        if (s == CWLB_OK) s = grow(&ctx->d_run_keys_sorted, 0, n_runs);
+        if (s == CWLB_OK) s = grow(&ctx->d_run_order, 0, n_runs);
+        if (s != CWLB_OK) {
+            ctx->run_cap = 0;
+            return s;
+        }
+        ctx->run_cap = n_runs;
+    }
+    const unsigned end_bit = std::max(1u, bits_for(static_cast<unsigned>(a.n_rows)));
+    rocprim::counting_iterator<int> ids(0);
+    size_t bytes = 0;
+    CWLB_HIP_TRY(rocprim::radix_sort_pairs(nullptr, bytes, ctx->d_run_keys, ctx->d_run_keys_sorted,
+                                           ids, ctx->d_run_order, n_runs, 0u, end_bit, st));
+    if (bytes > ctx->sort_temp_bytes || !ctx->d_sort_temp) {
+        if (ctx->d_sort_temp) CWLB_HIP_TRY(hipFree(ctx->d_sort_temp));
+        ctx->d_sort_temp = nullptr;
+        ctx->sort_temp_bytes = 0;
+        CWLB_HIP_TRY(hipMalloc(&ctx->d_sort_temp, bytes ? bytes : 1));
+        ctx->sort_temp_bytes = bytes;
+    }
+    const unsigned grid = static_cast<unsigned>((n_runs + kBlock - 1) / kBlock);
+    hipLaunchKernelGGL(run_keys, dim3(grid), dim3(kBlock), 0, st, a.tasks,
+                       static_cast<long long>(a.n_tasks), M, n_runs, a.origin, a.n_rows,
+                       ctx->d_run_keys);
+    CWLB_HIP_TRY(hipGetLastError());
+    bytes = ctx->sort_temp_bytes;
+    CWLB_HIP_TRY(rocprim::radix_sort_pairs(ctx->d_sort_temp, bytes, ctx->d_run_keys,
+                                           ctx->d_run_keys_sorted, ids, ctx->d_run_order, n_runs,
+                                           0u, end_bit, st));
+    *order = ctx->d_run_order;
+    return CWLB_OK;
+}
 
 cwlb_status launch_reorder(cwlb_ctx* ctx, int32_t n, int64_t nnz, const int32_t* rp,
                            const int32_t* ci, const float* val, int32_t* origin, int32_t* rp_out,

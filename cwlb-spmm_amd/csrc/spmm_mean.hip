@@ -221,15 +221,22 @@ __device__ __forceinline__ RunTask run_task(const cwlb_task* __restrict__ tasks,
     return r;
 }
 
-// Block b runs on XCD b % 8; slice = XCD % SL, and the blocks of one slice
-// enumerate the run blocks 0, 1, 2, ... (a bijection for SL in {1, 2, 4, 8}).
+// Block b runs on XCD b % 8; slice = XCD % SL.  The P = 8 / SL XCDs of one
+// slice share its run blocks [0, n_blocks), either interleaved (XCD q of the
+// slice takes blocks q, q + P, q + 2P, ...) or contiguous (XCD q takes
+// blocks [q * chunk, (q + 1) * chunk), chunk = ceil(n_blocks / P)), so that
+// each XCD's L2 sees one stretch of the run order.  Both are bijections from
+// the launched grid onto a superset of [0, n_blocks).
 template <int SL>
-__device__ __forceinline__ void block_slice(int& slice, long long& jb)
+__device__ __forceinline__ void block_slice(int& slice, long long& jb, long long chunk)
 {
+    constexpr int P = 8 / SL;
     const int bx = blockIdx.x;
     const int xcd = bx & 7;
     slice = xcd % SL;
-    jb = static_cast<long long>(bx >> 3) * (8 / SL) + xcd / SL;
+    const int q = xcd / SL;
+    jb = chunk > 0 ? static_cast<long long>(q) * chunk + (bx >> 3)
+                   : static_cast<long long>(bx >> 3) * P + q;
 }
 
 template <int VEC, int G, int R, int U, int SL>
@@ -238,7 +245,8 @@ spmm_mean_runs(const int* __restrict__ rp, const int* __restrict__ ci,
                const float* __restrict__ val, const int* __restrict__ origin, int n_rows,
                long long nnz, const float* __restrict__ H, long long h_rows, int ld,
                const cwlb_task* __restrict__ tasks, long long n_tasks, int M, long long n_runs,
-               long long n_blocks, float* __restrict__ C, int* __restrict__ status)
+               long long n_blocks, long long chunk, const int* __restrict__ run_order,
+               float* __restrict__ C, int* __restrict__ status)
 {
     using V = typename VecT<VEC>::T;
     constexpr int NS = 64 / G;                     // row slots per wave
@@ -253,10 +261,13 @@ spmm_mean_runs(const int* __restrict__ rp, const int* __restrict__ ci,
     const int sub = lane - slot * G;
     int slice;
     long long jb;
-    block_slice<SL>(slice, jb);
+    block_slice<SL>(slice, jb, chunk);
     if (jb >= n_blocks) return;
-    const long long run = jb * kWaves + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    if (run >= n_runs) return;
+    const long long pos = jb * kWaves + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if (pos >= n_runs) return;
+    // run_order (optional) is a permutation of [0, n_runs): runs execute in
+    // that order instead of task order.
+    const long long run = run_order ? static_cast<long long>(run_order[pos]) : pos;
 
     const RunTask tk = run_task(tasks, n_tasks, run, M);
     const int rs = tk.rs;
@@ -572,7 +583,10 @@ struct Plan {
     int M;
     long long runs;
     long long blocks;      // run blocks per slice
-    long long grid;        // launched blocks (slices x run blocks, padded to 8)
+    long long chunk;       // run blocks per XCD when contiguous, else 0
+    long long grid;        // launched blocks
+    bool ordered;          // runs execute sorted by output row id
+    const int* order;      // that order (device), set at launch
 };
 
 template <int VEC, int G, int R, int SL>
@@ -582,8 +596,8 @@ void launch_main(hipStream_t st, const SpmmArgs& a, const Plan& p, int* status)
     hipLaunchKernelGGL((spmm_mean_runs<VEC, G, R, U, SL>), dim3(static_cast<unsigned>(p.grid)),
                        dim3(kBlock), 0, st, a.row_ptr, a.col_idx, a.val, a.origin, a.n_rows,
                        static_cast<long long>(a.nnz), a.H, static_cast<long long>(a.h_rows), a.K,
-                       a.tasks, static_cast<long long>(a.n_tasks), p.M, p.runs, p.blocks, a.C,
-                       status);
+                       a.tasks, static_cast<long long>(a.n_tasks), p.M, p.runs, p.blocks, p.chunk,
+                       p.order, a.C, status);
 }
 
 template <int VEC, int SL>
@@ -648,10 +662,16 @@ int pick_vec(const SpmmArgs& a)
     return 1;
 }
 
-// Tasks per wave: enough runs for ~64 waves per CU, at most 64 tasks each.
-// Feature slices across XCDs: only with runs long enough to amortise the
-// per-run setup (M >= 8), and only when each slice is a whole number of
-// 128-byte lines.  The context's schedule overrides either choice.
+// Automatic schedule (the context's settings override each choice):
+//   * feature slices across XCDs only when the feature matrix is well beyond
+//     what the 256 MB Infinity Cache holds (>= 512 MB): then each XCD's L2
+//     caching one 128-byte slice of the hot rows pays; below that, slicing
+//     only multiplies the per-row work (measured: Chung-Lu K=64, H = 256 MB,
+//     10% slower with 2 slices; R-MAT K=128, H = 2 GB, 4-5% faster with 4);
+//   * tasks per wave M: the largest M that keeps at least 64 waves per CU
+//     (runs x slices) and at most ~256 rows per run (long runs of short rows
+//     serialise latency: the 16M-row mesh is 9% faster at 4 tasks per wave
+//     than at 16), clamped to [1, 64].
 Plan make_plan(const cwlb_ctx* ctx, const SpmmArgs& a, bool per_task)
 {
     Plan p{};
@@ -659,24 +679,36 @@ Plan make_plan(const cwlb_ctx* ctx, const SpmmArgs& a, bool per_task)
     p.M = 1;
     p.sl = 1;
     if (!per_task) {
-        if (ctx->sched_tasks_per_wave > 0) {
-            p.M = ctx->sched_tasks_per_wave;
-        } else {
-            const long long target = static_cast<long long>(std::max(ctx->compute_units, 1)) * 64;
-            p.M = static_cast<int>(
-                std::max<long long>(1, std::min<long long>(64, a.n_tasks / target)));
-        }
+        const long long h_bytes = a.h_rows * static_cast<long long>(a.K) * 4;
         if (ctx->sched_slices > 0) {
             p.sl = ctx->sched_slices;
-        } else if (p.M >= 8) {
+        } else if (h_bytes >= (512ll << 20)) {
             if (a.K % 128 == 0 && a.K >= 128 && a.K <= 512) p.sl = 4;
             else if (a.K % 64 == 0 && a.K >= 64 && a.K <= 256) p.sl = 2;
         }
         if (p.vec != 4 || a.K % (4 * p.sl) != 0) p.sl = 1;
+        if (ctx->sched_tasks_per_wave > 0) {
+            p.M = ctx->sched_tasks_per_wave;
+        } else {
+            const long long waves = static_cast<long long>(std::max(ctx->compute_units, 1)) * 64;
+            const long long m_par = a.n_tasks * p.sl / waves;
+            const long long m_rows = a.n_rows > 0 ? 256 * a.n_tasks / a.n_rows : 64;
+            p.M = static_cast<int>(std::max<long long>(1, std::min({m_par, m_rows, 64ll})));
+        }
     }
     p.runs = (a.n_tasks + p.M - 1) / p.M;
     p.blocks = (p.runs + kWaves - 1) / kWaves;
-    p.grid = p.sl == 1 ? p.blocks : (p.blocks * p.sl + 7) / 8 * 8;
+    const bool contiguous = !per_task && ctx->sched_xcd == 2;
+    if (contiguous) {
+        const long long P = 8 / p.sl;
+        p.chunk = (p.blocks + P - 1) / P;
+        p.grid = p.chunk * 8;
+    } else {
+        p.chunk = 0;
+        p.grid = p.sl == 1 ? p.blocks : (p.blocks * p.sl + 7) / 8 * 8;
+    }
+    p.ordered = !per_task && ctx->sched_order == 2 && p.runs > 1;
+    p.order = nullptr;
     return p;
 }
 
@@ -695,7 +727,11 @@ cwlb_status launch_spmm_mean(cwlb_ctx* ctx, const SpmmArgs& a, bool zero_all, bo
         hipLaunchKernelGGL(fill_zero, dim3(blocks), dim3(kBlock), 0, st, a.C,
                            std::max<long long>(total, 0), ctx->d_status);
     }
-    const Plan p = make_plan(ctx, a, per_task);
+    Plan p = make_plan(ctx, a, per_task);
+    if (p.ordered && a.n_tasks > 0 && a.K > 0) {
+        const cwlb_status s = build_run_order(ctx, a, p.M, p.runs, &p.order);
+        if (s != CWLB_OK) return s;
+    }
     if (!zero_all && a.n_tasks > 0 && a.K > 0) {
         if (p.vec == 4) launch_zero<4>(st, a, p, ctx->d_status);
         else if (p.vec == 2) launch_zero<2>(st, a, p, ctx->d_status);

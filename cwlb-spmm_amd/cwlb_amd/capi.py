@@ -23,6 +23,7 @@ PER_TASK = 0x2
 EXPORTS = [
     "cwlb_version", "cwlb_last_error", "cwlb_ctx_create", "cwlb_ctx_destroy",
     "cwlb_ctx_set_stream", "cwlb_ctx_synchronize", "cwlb_ctx_device_info", "cwlb_ctx_set_schedule",
+    "cwlb_ctx_set_locality",
     "cwlb_spmm_mean_f32", "cwlb_spmm_mean_f32_large_k", "cwlb_spmm_mean_f32_host",
     "cwlb_reorder_by_degree", "cwlb_reorder_by_degree_device", "cwlb_partition",
     "cwlb_capacity_from_s", "cwlb_wave_based_s", "cwlb_recommended_candidate_w",
@@ -96,6 +97,7 @@ def lib():
         L.cwlb_ctx_synchronize.argtypes = [vp]
         L.cwlb_ctx_device_info.argtypes = [vp, C.POINTER(DeviceInfo)]
         L.cwlb_ctx_set_schedule.argtypes = [vp, i32, i32]
+        L.cwlb_ctx_set_locality.argtypes = [vp, i32, i32]
         spmm = [vp, vp, vp, vp, vp, i32, i64, vp, i64, i32, vp, i64, vp, u32, C.POINTER(Timing)]
         L.cwlb_spmm_mean_f32.argtypes = spmm
         L.cwlb_spmm_mean_f32_large_k.argtypes = spmm
@@ -255,6 +257,9 @@ class Context:
 
     def set_schedule(self, tasks_per_wave=0, feature_slices=0):
         check(lib().cwlb_ctx_set_schedule(self.h, int(tasks_per_wave), int(feature_slices)))
+
+    def set_locality(self, run_order=0, xcd_blocks=0):
+        check(lib().cwlb_ctx_set_locality(self.h, int(run_order), int(xcd_blocks)))
 
     def synchronize(self):
         check(lib().cwlb_ctx_synchronize(self.h))

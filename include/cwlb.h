@@ -108,6 +108,16 @@ cwlb_status cwlb_ctx_device_info(cwlb_ctx* ctx, cwlb_device_info* out);
  * fixed); tuning and tests use it. */
 cwlb_status cwlb_ctx_set_schedule(cwlb_ctx* ctx, int32_t tasks_per_wave, int32_t feature_slices);
 
+/* Locality of later SpMM calls on this context.  run_order: 0 automatic,
+ * 1 runs in task order, 2 runs sorted by the original id of their first row
+ * (computed on the device at each call; groups the rows of all degree
+ * classes that neighbour each other in the original numbering).
+ * xcd_blocks: 0 automatic, 1 consecutive run blocks interleaved over the 8
+ * XCDs, 2 each XCD takes one contiguous stretch of run blocks.  Ignored with
+ * CWLB_SPMM_PER_TASK.  No counterpart in the reference; tuning and tests use
+ * it. */
+cwlb_status cwlb_ctx_set_locality(cwlb_ctx* ctx, int32_t run_order, int32_t xcd_blocks);
+
 /* ------------------------------------------------------------ aggregation
  * C[Origin_local[r]][k] = (sum over the task chunks of row r of
  *   val[j] * H[col_idx[j]][k]) / deg(r)

@@ -50,19 +50,25 @@ def run_gpu(ctx, p, H, flags=0, c_fill=float("nan"), large_k=False, h_dev=None):
     return C[:p.n, :K].cpu().numpy(), t
 
 
-# (tasks_per_wave, feature_slices, flags): automatic, the reference's one task
-# per wave, and forced task-run fusion / XCD feature slicing (small graphs do
-# not trigger them automatically).
-SCHEDULES = [(0, 0, 0), (0, 0, capi.PER_TASK), (3, 1, 0), (8, 2, 0), (16, 4, 0), (64, 4, 0)]
-SCHED_IDS = ["auto", "per_task", "m3", "m8s2", "m16s4", "m64s4"]
+# (tasks_per_wave, feature_slices, flags, run_order, xcd_blocks): automatic,
+# the reference's one task per wave, forced task-run fusion / XCD feature
+# slicing (small graphs do not trigger them automatically), runs sorted by
+# output row and contiguous XCD stretches.
+SCHEDULES = [(0, 0, 0, 0, 0), (0, 0, capi.PER_TASK, 0, 0), (3, 1, 0, 1, 1), (8, 2, 0, 1, 1),
+             (16, 4, 0, 1, 1), (64, 4, 0, 1, 1), (2, 1, 0, 2, 1), (5, 1, 0, 1, 2),
+             (8, 4, 0, 2, 2), (1, 2, 0, 2, 2)]
+SCHED_IDS = ["auto", "per_task", "m3", "m8s2", "m16s4", "m64s4", "m2ord", "m5xcd", "m8s4ordxcd",
+             "m1s2ordxcd"]
 
 
 @pytest.fixture(params=SCHEDULES, ids=SCHED_IDS)
 def sched(request, gpu_ctx):
-    m, sl, flags = request.param
+    m, sl, flags, order, xcd = request.param
     gpu_ctx.set_schedule(m, sl)
+    gpu_ctx.set_locality(order, xcd)
     yield flags
     gpu_ctx.set_schedule(0, 0)
+    gpu_ctx.set_locality(0, 0)
 
 
 def check(got, ref):
@@ -419,3 +425,49 @@ def test_device_features_match_host(gpu_ctx):
         gpu_ctx.fill_features(H, rows, K, 42)
         assert np.array_equal(H.cpu().numpy(), synth.features(rows, K, 42))
         assert np.array_equal(features_rows(np.arange(rows), K, 42), synth.features(rows, K, 42))
+
+
+def test_schedule_and_locality_arguments(gpu_ctx):
+    for bad in ((-1, 0), (0, 3), (0, 16)):
+        with pytest.raises(capi.CwlbError) as e:
+            gpu_ctx.set_schedule(*bad)
+        assert e.value.status == capi.INVALID_ARG
+    for bad in ((3, 0), (-1, 0), (0, 3), (0, -2)):
+        with pytest.raises(capi.CwlbError) as e:
+            gpu_ctx.set_locality(*bad)
+        assert e.value.status == capi.INVALID_ARG
+    gpu_ctx.set_schedule(0, 0)
+    gpu_ctx.set_locality(0, 0)
+
+
+@pytest.mark.parametrize("cfg", [4, 5])
+def test_full_config_locality_modes_agree(gpu_ctx, cfg):
+    """Runs sorted by output row and contiguous XCD stretches give the same
+    result as the default schedule on the full-size graphs (within the
+    parity tolerance: only split-row atomic order differs)."""
+    torch = torch_mod()
+    g = workloads.graph(cfg)
+    K = workloads.FEATURE_DIM[cfg]
+    S = workloads.candidate_s(g.nnz, 256)[2]
+    p = problem(g, SKEWED_COSTS, S)
+    print(f"cfg={cfg} n={g.n} nnz={g.nnz} K={K} S={S}", flush=True)
+    d_rp, d_ci, d_v, d_o = dev(p.row_ptr), dev(p.col_idx), dev(p.val), dev(p.origin)
+    d_t = dev(np.ascontiguousarray(p.tasks, np.int32).reshape(-1))
+    H = torch.empty((g.n, K), dtype=torch.float32, device="cuda")
+    gpu_ctx.fill_features(H, g.n, K, workloads.FEATURE_SEED)
+    C0 = torch.full((g.n, K), float("nan"), dtype=torch.float32, device="cuda")
+    gpu_ctx.spmm(d_rp, d_ci, d_v, d_o, g.n, g.nnz, H, g.n, K, d_t, len(p.tasks), C0)
+    C1 = torch.full_like(C0, float("nan"))
+    try:
+        for m, order, xcd in ((4, 2, 1), (8, 2, 2), (32, 1, 2)):
+            gpu_ctx.set_schedule(m, 0)
+            gpu_ctx.set_locality(order, xcd)
+            C1.fill_(float("nan"))
+            gpu_ctx.spmm(d_rp, d_ci, d_v, d_o, g.n, g.nnz, H, g.n, K, d_t, len(p.tasks), C1)
+            diff = (C1 - C0).abs()
+            bound = RTOL * C0.abs() + ATOL
+            assert not torch.isnan(C1).any().item()
+            assert bool((diff <= bound).all().item()), (m, order, xcd, diff.max().item())
+    finally:
+        gpu_ctx.set_schedule(0, 0)
+        gpu_ctx.set_locality(0, 0)
