@@ -116,6 +116,9 @@ cwlb_status time_launches(cwlb_ctx* ctx, int repeat, Launch launch, Before befor
 template <class T>
 struct Buf {
     T* p = nullptr;
+    Buf() = default;
+    Buf(const Buf&) = delete;
+    Buf& operator=(const Buf&) = delete;
     ~Buf()
     {
         if (p) (void)hipFree(p);

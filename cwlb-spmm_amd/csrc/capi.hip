@@ -89,6 +89,9 @@ cwlb_status run_spmm(cwlb_ctx* ctx, const SpmmArgs& a, uint32_t flags, cwlb_timi
 template <class T>
 struct DevBuf {
     T* p = nullptr;
+    DevBuf() = default;
+    DevBuf(const DevBuf&) = delete;
+    DevBuf& operator=(const DevBuf&) = delete;
     ~DevBuf()
     {
         if (p) (void)hipFree(p);
@@ -321,6 +324,18 @@ cwlb_status cwlb_reorder_by_degree_device(cwlb_ctx* ctx, int32_t n_rows, int64_t
     DeviceGuard g(ctx->device);
     return launch_reorder(ctx, n_rows, nnz, row_ptr, col_idx, val, origin, row_ptr_out,
                           col_idx_out, val_out);
+}
+
+cwlb_status cwlb_partition_device(cwlb_ctx* ctx, const int32_t* row_ptr, int32_t n_rows,
+                                  const cwlb_cost_params* costs, double capacity_weight,
+                                  cwlb_task* out, int64_t capacity_tasks, int64_t* n_tasks)
+{
+    if (!ctx || !costs || !n_tasks) return fail(CWLB_INVALID_ARG, "cwlb_partition_device: null argument");
+    if (n_rows > 0 && !row_ptr) return fail(CWLB_INVALID_ARG, "cwlb_partition_device: null row_ptr");
+    if (capacity_tasks < 0) return fail(CWLB_INVALID_ARG, "cwlb_partition_device: negative capacity");
+    DeviceGuard g(ctx->device);
+    return launch_partition(ctx, row_ptr, n_rows, costs, capacity_weight, out, capacity_tasks,
+                            n_tasks);
 }
 
 cwlb_status cwlb_calibrate(cwlb_ctx* ctx, int32_t K, int32_t repeat, int32_t WI, int32_t load_MB,

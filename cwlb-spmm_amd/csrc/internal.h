@@ -52,6 +52,13 @@ cwlb_status hip_fail(hipError_t e, const char* what);
         if (e_ != hipSuccess) return ::cwlb::hip_fail(e_, #expr); \
     } while (0)
 
+// Checks the launch just enqueued, naming it in the error message.
+#define CWLB_LAUNCH_CHECK(name)                                                    \
+    do {                                                                           \
+        hipError_t e_ = hipGetLastError();                                         \
+        if (e_ != hipSuccess) return ::cwlb::hip_fail(e_, "launch of " name);      \
+    } while (0)
+
 // Scoped device switch.
 struct DeviceGuard {
     int prev = -1;
@@ -92,6 +99,12 @@ cwlb_status launch_spmm_mean(cwlb_ctx* ctx, const SpmmArgs& a, bool zero_all, bo
 // ctx->stream; *order receives ctx->d_run_order.
 cwlb_status build_run_order(cwlb_ctx* ctx, const SpmmArgs& a, int M, long long n_runs,
                             const int** order);
+
+// The GPU partition (csrc/partition.hip): row_ptr and out are device
+// arrays; synchronises.
+cwlb_status launch_partition(cwlb_ctx* ctx, const int32_t* row_ptr, int32_t n_rows,
+                             const cwlb_cost_params* costs, double capacity_weight,
+                             cwlb_task* out, int64_t capacity_tasks, int64_t* n_tasks);
 
 cwlb_status launch_fill_features(cwlb_ctx* ctx, float* H, int64_t rows, int32_t K, uint64_t seed);
 

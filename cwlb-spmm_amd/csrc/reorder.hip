@@ -85,6 +85,9 @@ __global__ void set_first_zero(int* __restrict__ p) { p[0] = 0; }
 
 struct DevMem {
     void* p = nullptr;
+    DevMem() = default;
+    DevMem(const DevMem&) = delete;
+    DevMem& operator=(const DevMem&) = delete;
     ~DevMem()
     {
         if (p) (void)hipFree(p);
@@ -171,6 +174,7 @@ cwlb_status launch_reorder(cwlb_ctx* ctx, int32_t n, int64_t nnz, const int32_t*
                            int32_t* ci_out, float* val_out)
 {
     hipStream_t st = ctx->stream;
+    (void)hipGetLastError();  // report only the launches below
     if (n == 0) {
         if (!rp_out) return fail(CWLB_INVALID_ARG, "reorder: null row_ptr_out");
         hipLaunchKernelGGL(set_first_zero, dim3(1), dim3(1), 0, st, rp_out);

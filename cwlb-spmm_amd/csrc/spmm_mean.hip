@@ -718,6 +718,7 @@ cwlb_status launch_spmm_mean(cwlb_ctx* ctx, const SpmmArgs& a, bool zero_all, bo
                              bool record_events)
 {
     hipStream_t st = ctx->stream;
+    (void)hipGetLastError();  // report only the launches below
     if (record_events) CWLB_HIP_TRY(hipEventRecord(ctx->ev[0], st));
     const long long total = static_cast<long long>(a.n_rows) * a.K;
     if (zero_all) {

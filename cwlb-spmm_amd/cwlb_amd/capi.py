@@ -26,6 +26,7 @@ EXPORTS = [
     "cwlb_ctx_set_locality",
     "cwlb_spmm_mean_f32", "cwlb_spmm_mean_f32_large_k", "cwlb_spmm_mean_f32_host",
     "cwlb_reorder_by_degree", "cwlb_reorder_by_degree_device", "cwlb_partition",
+    "cwlb_partition_device",
     "cwlb_capacity_from_s", "cwlb_wave_based_s", "cwlb_recommended_candidate_w",
     "cwlb_candidate_search_bounds", "cwlb_candidate_search_by_count",
     "cwlb_candidate_search_by_step", "cwlb_calibrate", "cwlb_save_costs", "cwlb_read_costs",
@@ -107,6 +108,8 @@ def lib():
         L.cwlb_reorder_by_degree_device.argtypes = [vp, i32, i64, vp, vp, vp, vp, vp, vp, vp]
         L.cwlb_partition.argtypes = [vp, i32, C.POINTER(CostParams), C.c_double, vp, i64,
                                      C.POINTER(i64)]
+        L.cwlb_partition_device.argtypes = [vp, vp, i32, C.POINTER(CostParams), C.c_double, vp,
+                                            i64, C.POINTER(i64)]
         L.cwlb_capacity_from_s.argtypes = [i32, C.POINTER(CostParams)]
         L.cwlb_capacity_from_s.restype = C.c_double
         L.cwlb_wave_based_s.argtypes = [i64, i64, i32, i32, C.POINTER(i32)]
@@ -301,6 +304,25 @@ class Context:
         check(lib().cwlb_reorder_by_degree_device(self.h, int(n_rows), int(nnz), _ptr(row_ptr),
                                                   _ptr(col_idx), _ptr(val), _ptr(origin),
                                                   _ptr(rp_out), _ptr(ci_out), _ptr(v_out)))
+
+    def partition_device(self, row_ptr, n_rows, costs4, capacity, out, capacity_tasks):
+        """cwlb_partition_device on device arrays; returns the task count."""
+        cp = costs(costs4)
+        cnt = i64()
+        check(lib().cwlb_partition_device(self.h, _ptr(row_ptr), int(n_rows), C.byref(cp),
+                                          float(capacity), _ptr(out), int(capacity_tasks),
+                                          C.byref(cnt)))
+        return cnt.value
+
+    def partition_device_count(self, row_ptr, n_rows, costs4, capacity):
+        """Task count only (the INSUFFICIENT sizing call)."""
+        cp = costs(costs4)
+        cnt = i64()
+        st = lib().cwlb_partition_device(self.h, _ptr(row_ptr), int(n_rows), C.byref(cp),
+                                         float(capacity), None, 0, C.byref(cnt))
+        if st not in (OK, INSUFFICIENT):
+            check(st)
+        return cnt.value
 
     def calibrate(self, K=128, repeat=500, WI=131072, load_MB=512, atomic_writers=8):
         cp = CostParams()

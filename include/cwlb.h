@@ -209,6 +209,20 @@ cwlb_status cwlb_partition(const int32_t* row_ptr, int32_t n_rows, const cwlb_co
                            double capacity_weight, cwlb_task* out, int64_t capacity_tasks,
                            int64_t* n_tasks);
 
+/* The same partition computed on the GPU from the device offsets
+ * row_ptr[n_rows + 1] into the device array out; identical task lists.
+ * Each fresh state of the host's greedy state machine (a task opening at a
+ * row, or at a long row whose deg % S prefix went to the previous task) is
+ * simulated to the next one in parallel, and the chain from row 0 is found
+ * by pointer doubling.  Returns CWLB_INSUFFICIENT (with *n_tasks set) when
+ * capacity_tasks is too small, and CWLB_UNSUPPORTED for costs under which a
+ * task's row count has no bound (C_store <= 0, C_compute + C_load < 0,
+ * non-finite values, capacity / C_store > 65536): cwlb_partition handles
+ * those.  row_ptr must be non-decreasing.  Synchronises. */
+cwlb_status cwlb_partition_device(cwlb_ctx* ctx, const int32_t* row_ptr, int32_t n_rows,
+                                  const cwlb_cost_params* costs, double capacity_weight,
+                                  cwlb_task* out, int64_t capacity_tasks, int64_t* n_tasks);
+
 /* --------------------------------------------------- segment-size selection
  * capacity_from_s (reference main.cpp:281-292). */
 double cwlb_capacity_from_s(int32_t s, const cwlb_cost_params* costs);

@@ -29,6 +29,11 @@
 //   posarg TEXT                        positive_search_argument
 //   costs-save PATH APPEND PREC CC CL CS CA / costs-read PATH
 //   device                             cwlb::Device properties
+//   partition-emul ORDER CC CL CS CA S OUT   the GPU partition's algorithm
+//                                      (fresh-node transitions, pointer doubling,
+//                                      chain expansion) run on the host
+#include <climits>
+#include <cmath>
 #include <cstdint>
 #include <cstdio>
 #include <cstdlib>
@@ -43,6 +48,7 @@
 
 #include "cwlb_driver.h"
 #include "data.h"
+#include "partition_sim.h"
 #include "parallelMatrix.h"
 #include "utils.h"
 
@@ -157,6 +163,85 @@ SpmmCostParams costs_from(char** a)
     return c;
 }
 
+// The GPU partition's steps (csrc/partition.hip) executed sequentially with
+// the same per-node simulation, so the decomposition and the doubling are
+// checked on the host.
+std::vector<ParallelDataWeighted> partition_emulated(const std::vector<int>& rp,
+                                                     const SpmmCostParams& c, double cap)
+{
+    namespace P = cwlb::part;
+    const int n = static_cast<int>(rp.size()) - 1;
+    std::vector<ParallelDataWeighted> out;
+    if (n <= 0) return out;
+    P::PartParams p{};
+    p.rp = rp.data();
+    p.n = n;
+    p.wcl = c.C_compute_ns + c.C_load_ns;
+    p.cs = c.C_store_ns;
+    p.ca = c.C_atomic_ns;
+    p.cap = cap;
+    const double denom = (1e-30 < p.wcl) ? p.wcl : 1e-30;
+    const double x = std::floor((cap - p.ca) / denom);
+    int s = INT_MIN;
+    if (x == x && x < 2147483648.0 && x > -2147483649.0) s = static_cast<int>(x);
+    p.S = std::max(1, s);
+    if (!(p.cs > 0.0) || !(p.wcl >= 0.0) || !std::isfinite(cap) || cap / p.cs > 65536.0)
+        throw std::invalid_argument("partition-emul: unsupported costs");
+    p.max_scan = static_cast<long long>(cap / p.cs * (1.0 + 1e-6)) + 4;
+    std::vector<int> long_idx(static_cast<std::size_t>(n), -1), long_row;
+    for (int r = 0; r < n; ++r)
+        if (!(P::full_w(p, r) <= cap)) {
+            long_idx[static_cast<std::size_t>(r)] = static_cast<int>(long_row.size());
+            long_row.push_back(r);
+        }
+    p.long_row = long_row.data();
+    p.long_idx = long_idx.data();
+    const long long V = n + 1 + static_cast<long long>(long_row.size());
+    std::vector<std::vector<int>> J(1, std::vector<int>(static_cast<std::size_t>(V)));
+    std::vector<int> cnt(static_cast<std::size_t>(V));
+    for (long long v = 0; v < V; ++v) {
+        P::Emitter em{nullptr, 0};
+        int overrun = 0;
+        J[0][static_cast<std::size_t>(v)] = P::simulate(p, static_cast<int>(v), em, &overrun);
+        cnt[static_cast<std::size_t>(v)] = static_cast<int>(em.count);
+        if (overrun) throw std::runtime_error("partition-emul: scan overrun");
+    }
+    while (J.back()[0] != n) {
+        const std::vector<int>& a = J.back();
+        std::vector<int> b(a.size());
+        for (std::size_t v = 0; v < a.size(); ++v) b[v] = a[static_cast<std::size_t>(a[v])];
+        J.push_back(std::move(b));
+    }
+    const long long len = 1LL << (J.size() - 1);
+    std::vector<int> chain(static_cast<std::size_t>(len), 0);
+    for (int j = static_cast<int>(J.size()) - 2; j >= 0; --j) {
+        const long long half = 1LL << j;
+        for (long long pos = 0; pos < len; pos += 2 * half)
+            chain[static_cast<std::size_t>(pos + half)] =
+                J[static_cast<std::size_t>(j)][static_cast<std::size_t>(chain[static_cast<std::size_t>(pos)])];
+    }
+    long long total = 0;
+    std::vector<long long> off(static_cast<std::size_t>(len));
+    for (long long i = 0; i < len; ++i) {
+        off[static_cast<std::size_t>(i)] = total;
+        const int v = chain[static_cast<std::size_t>(i)];
+        if (v != n) total += cnt[static_cast<std::size_t>(v)];
+    }
+    std::vector<cwlb_task> tasks(static_cast<std::size_t>(total));
+    for (long long i = 0; i < len; ++i) {
+        const int v = chain[static_cast<std::size_t>(i)];
+        if (v == n) continue;
+        P::Emitter em{tasks.data() + off[static_cast<std::size_t>(i)], 0};
+        int overrun = 0;
+        (void)P::simulate(p, v, em, &overrun);
+        if (em.count != cnt[static_cast<std::size_t>(v)])
+            throw std::runtime_error("partition-emul: emitted and counted tasks differ");
+    }
+    for (const cwlb_task& t : tasks)
+        out.push_back(ParallelDataWeighted{t.row_start, t.row_end, t.first_row_offset, t.last_row_nnz});
+    return out;
+}
+
 int run(int argc, char** argv)
 {
     if (argc < 2) throw std::invalid_argument("probe: no subcommand");
@@ -180,6 +265,15 @@ int run(int argc, char** argv)
         const SpmmCostParams c = costs_from(argv + 3);
         const double cap = capacity_from_s(std::stoi(argv[7]), c);
         const std::vector<ParallelDataWeighted> t = costWeightedTaskPartitioning(o, c, cap);
+        Writer w(argv[8]);
+        w.one(cap);
+        w.put(t);
+    } else if (cmd == "partition-emul") {
+        need(7);
+        const CSR_Order o = read_order(argv[2]);
+        const SpmmCostParams c = costs_from(argv + 3);
+        const double cap = capacity_from_s(std::stoi(argv[7]), c);
+        const std::vector<ParallelDataWeighted> t = partition_emulated(o.RowOffset, c, cap);
         Writer w(argv[8]);
         w.one(cap);
         w.put(t);

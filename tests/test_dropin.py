@@ -368,3 +368,56 @@ def test_cost_write_argument_errors(tmp_path, args, msg):
     r = run_exe("costWrite", *args, cwd=tmp_path)
     assert r.returncode == 1
     assert msg in r.stderr
+
+
+# ------------------------------------------- GPU partition's decomposition
+def run_partition_emul(tmp_path, order, costs, S):
+    write_order(tmp_path / "ord", *order)
+    probe("partition-emul", tmp_path / "ord", *costs, S, tmp_path / "tasks")
+    raw = open(tmp_path / "tasks", "rb").read()
+    return np.frombuffer(raw[8:], np.int32).reshape(-1, 4)
+
+
+@pytest.mark.parametrize("degs,expected", APPENDIX_A)
+def test_partition_decomposition_known_answers(tmp_path, degs, expected):
+    tasks = run_partition_emul(tmp_path, order_from_degrees(degs), UNIT_COSTS, 4)
+    assert [tuple(t) for t in tasks] == expected
+
+
+def test_partition_decomposition_random(tmp_path, rng):
+    """Fresh-node transitions + pointer doubling + chain expansion (the GPU
+    partition's algorithm, run on the host) reproduce the sequential
+    partition on random degree sequences, including degree-0 rows, long
+    rows next to each other and remainders that do and do not fit."""
+    checked = 0
+    for trial in range(200):
+        n = int(rng.integers(1, 80))
+        kind = trial % 3
+        if kind == 0:
+            degs = rng.integers(0, 12, n)
+        elif kind == 1:
+            degs = np.sort(rng.geometric(0.15, n) - 1)
+        else:
+            degs = rng.integers(0, 40, n)
+            degs[rng.random(n) < 0.2] = 0
+        order = order_from_degrees(degs)
+        costs = [(0.25, 0.75, 0.5, 0.5), (0.125, 1.375, 0.75, 3.5),
+                 (0.004519, 0.015617, 0.010667, 0.540499)][trial % 3]
+        for S in (1, 2, 3, 5, 8, 13):
+            got = run_partition_emul(tmp_path, order, costs, S)
+            cap = oracle.capacity_from_s(S, costs)
+            assert np.array_equal(got, oracle.partition(order[1], costs, cap)), (trial, S, degs)
+            checked += 1
+    assert checked == 1200
+
+
+@pytest.mark.parametrize("cfg", [1, 2, 3, 4, 5])
+def test_partition_decomposition_workloads(tmp_path, cfg):
+    g = workloads.small(cfg)
+    order = oracle.reorder_by_degree(g.row_ptr, g.col_idx, g.val)
+    for S in workloads.candidate_s(g.nnz, 256) + [1, 4]:
+        got = run_partition_emul(tmp_path, order, SKEWED_COSTS, S)
+        cap = oracle.capacity_from_s(S, SKEWED_COSTS)
+        assert np.array_equal(got, oracle.partition(order[1], SKEWED_COSTS, cap))
+        if REF is not None:
+            assert np.array_equal(got, oracle.ref_partition(order[1], SKEWED_COSTS, cap))

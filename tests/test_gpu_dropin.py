@@ -305,3 +305,84 @@ def test_cost_write_small(tmp_path):
     assert "Saved cost parameters to: ../resources/spmm_costs.txt" in r.stdout
     vals = [float(x) for x in (tmp_path / "resources" / "spmm_costs.txt").read_text().split()]
     assert len(vals) == 4 and all(v > 0 for v in vals)
+
+
+# ------------------------------------------------------------ GPU partition
+def device_partition(ctx, rp, costs, cap):
+    import torch
+    n = len(rp) - 1
+    d_rp = dev(np.asarray(rp, np.int32))
+    T = ctx.partition_device_count(d_rp, n, costs, cap)
+    out = torch.full((max(T, 1), 4), -9, dtype=torch.int32, device="cuda")
+    T2 = ctx.partition_device(d_rp, n, costs, cap, out, T)
+    assert T2 == T
+    return out.cpu().numpy()[:T]
+
+
+@pytest.mark.parametrize("cfg", [1, 2, 3, 4, 5])
+def test_device_partition_small(gpu_ctx, cfg):
+    g = workloads.small(cfg)
+    _, rp, _, _ = capi.reorder_by_degree(g.row_ptr, g.col_idx, g.val)
+    for costs in (UNIT_COSTS, SKEWED_COSTS, (0.004519, 0.015617, 0.010667, 0.540499)):
+        for S in workloads.candidate_s(g.nnz, 256) + [1, 3]:
+            cap = capi.capacity_from_s(S, costs)
+            got = device_partition(gpu_ctx, rp, costs, cap)
+            assert np.array_equal(got, capi.partition(rp, costs, cap)), (cfg, costs, S)
+
+
+@pytest.mark.parametrize("cfg", [2, 3, 4, 5])
+def test_device_partition_full(gpu_ctx, cfg):
+    """Full-size graphs at the three wave-based S with the gfx950 costs:
+    task-for-task identical to the host partition."""
+    import time
+    g = workloads.graph(cfg)
+    _, rp, _, _ = capi.reorder_by_degree(g.row_ptr, g.col_idx, g.val)
+    costs = (0.004519, 0.015617, 0.010667, 0.540499)
+    for S in workloads.candidate_s(g.nnz, 256):
+        cap = capi.capacity_from_s(S, costs)
+        t0 = time.perf_counter()
+        got = device_partition(gpu_ctx, rp, costs, cap)
+        t1 = time.perf_counter()
+        exp = capi.partition(rp, costs, cap)
+        t2 = time.perf_counter()
+        print(f"cfg={cfg} S={S} T={len(exp)} device {1e3 * (t1 - t0):.1f} ms (two calls) "
+              f"host {1e3 * (t2 - t1):.1f} ms", flush=True)
+        assert np.array_equal(got, exp)
+
+
+def test_device_partition_random(gpu_ctx, rng):
+    for trial in range(60):
+        n = int(rng.integers(1, 3000))
+        degs = rng.geometric(0.05, n) - 1
+        if trial % 2:
+            degs = np.sort(degs)
+        degs[rng.random(n) < 0.3] = 0
+        rp = np.concatenate([[0], np.cumsum(degs)]).astype(np.int32)
+        costs = (UNIT_COSTS, SKEWED_COSTS)[trial % 2]
+        S = int(rng.integers(1, 60))
+        cap = capi.capacity_from_s(S, costs)
+        assert np.array_equal(device_partition(gpu_ctx, rp, costs, cap),
+                              capi.partition(rp, costs, cap)), (trial, S)
+
+
+def test_device_partition_edge_cases(gpu_ctx):
+    import torch
+    # no rows
+    assert gpu_ctx.partition_device_count(dev(np.zeros(1, np.int32)), 0, UNIT_COSTS, 4.5) == 0
+    # one row, a single hub row, all rows empty
+    for degs in ([0], [7], [100000], [0] * 500, [3, 0, 0, 9, 1000, 5]):
+        rp = np.concatenate([[0], np.cumsum(degs)]).astype(np.int32)
+        cap = capi.capacity_from_s(4, UNIT_COSTS)
+        assert np.array_equal(device_partition(gpu_ctx, rp, UNIT_COSTS, cap),
+                              capi.partition(rp, UNIT_COSTS, cap))
+    # a buffer too small reports the count
+    rp = np.concatenate([[0], np.cumsum([5] * 50)]).astype(np.int32)
+    out = torch.zeros((2, 4), dtype=torch.int32, device="cuda")
+    with pytest.raises(capi.CwlbError) as e:
+        gpu_ctx.partition_device(dev(rp), 50, UNIT_COSTS, 4.5, out, 2)
+    assert e.value.status == capi.INSUFFICIENT
+    # costs with no bound on a task's row count stay with the host partition
+    for costs in ((0.25, 0.75, 0.0, 0.5), (0.25, -0.75, 0.5, 0.5), (0.25, 0.75, 1e-9, 0.5)):
+        with pytest.raises(capi.CwlbError) as e:
+            gpu_ctx.partition_device_count(dev(rp), 50, costs, capi.capacity_from_s(4, costs))
+        assert e.value.status == capi.UNSUPPORTED
