@@ -46,6 +46,49 @@ def measured_traffic():
     return float(m.group(1)) if m else None
 
 
+def preprocessing_times(ctx, g, rp, costs, S, tasks, reorder_host_ms):
+    """Wall times (ms) of the degree reordering and the partition at S, on
+    the host and on the GPU (outside the timed region; results checked
+    equal)."""
+    import numpy as np
+    import torch
+
+    from cwlb_amd import capi
+
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()  # noqa: E731
+    n, nnz = g.n, g.nnz
+    d_rp0, d_ci0, d_v0 = dev(g.row_ptr), dev(g.col_idx), dev(g.val)
+    outs = [torch.empty(n, dtype=torch.int32, device="cuda"),
+            torch.empty(n + 1, dtype=torch.int32, device="cuda"),
+            torch.empty(max(nnz, 1), dtype=torch.int32, device="cuda"),
+            torch.empty(max(nnz, 1), dtype=torch.float32, device="cuda")]
+    ctx.reorder_device(n, nnz, d_rp0, d_ci0, d_v0, *outs)  # warm-up
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ctx.reorder_device(n, nnz, d_rp0, d_ci0, d_v0, *outs)
+    reorder_dev_ms = (time.perf_counter() - t0) * 1e3
+    same_rp = bool(np.array_equal(outs[1].cpu().numpy(), rp))
+    del d_ci0, d_v0, outs
+    cap = capi.capacity_from_s(S, costs)
+    t0 = time.perf_counter()
+    host_tasks = capi.partition(rp, costs, cap)
+    part_host_ms = (time.perf_counter() - t0) * 1e3
+    d_rp = dev(rp)
+    out = torch.empty((len(host_tasks), 4), dtype=torch.int32, device="cuda")
+    try:
+        ctx.partition_device(d_rp, n, costs, cap, out, len(host_tasks))  # warm-up
+        t0 = time.perf_counter()
+        ctx.partition_device(d_rp, n, costs, cap, out, len(host_tasks))
+        part_dev_ms = round((time.perf_counter() - t0) * 1e3, 2)
+        same_tasks = bool(np.array_equal(out.cpu().numpy(), host_tasks))
+    except capi.CwlbError as e:
+        part_dev_ms, same_tasks = str(e), None
+    return {"reorder_host_ms": round(reorder_host_ms, 1), "reorder_device_ms": round(reorder_dev_ms, 2),
+            "reorder_identical": same_rp, "partition_host_ms": round(part_host_ms, 1),
+            "partition_device_ms": part_dev_ms, "partition_identical": same_tasks,
+            "tasks_identical_to_bench_tasks": bool(np.array_equal(host_tasks, tasks))}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -79,9 +122,11 @@ def main():
     t0 = time.time()
     g = workloads.graph(cfg)
     log(f"graph {workloads.NAMES[cfg]}: n={g.n} nnz={g.nnz} ({time.time() - t0:.1f}s)")
+    t0 = time.perf_counter()
     origin, rp, ci, val = capi.reorder_by_degree(g.row_ptr, g.col_idx, g.val)
+    reorder_host_ms = (time.perf_counter() - t0) * 1e3
     costs = capi.read_costs(args.costs)
-    log(f"reordered; costs {costs}")
+    log(f"reordered on the host in {reorder_host_ms:.0f} ms; costs {costs}")
 
     stream = torch.cuda.current_stream()
     ctx = capi.Context(0, stream.cuda_stream)
@@ -113,6 +158,8 @@ def main():
             best = (S, us, tk, d_t)
     S, _, tasks, d_t = best
     T = len(tasks)
+    prep = preprocessing_times(ctx, g, rp, costs, S, tasks, reorder_host_ms)
+    log(f"preprocessing: {prep}")
 
     # Timed region: W warm-ups, K steps, synchronised on both sides.
     for _ in range(args.warmup):
@@ -209,6 +256,7 @@ def main():
                    "main_kernel_us": round(main_us, 2), "zero_pass_us": round(zero_us, 2),
                    "per_task_mode_us": round(per_task_us, 2),
                    "host_pointer_call_ms": None if host_call_ms is None else round(host_call_ms, 1),
+                   "preprocessing": prep,
                    "algorithmic_bytes": b_alg},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),

@@ -151,8 +151,9 @@ SingleSResult run_single_s(cwlb::Device& queue, const CSR_Order& csr,
     SingleSResult result;
     result.s = s;
     result.capacity = capacity_from_s(s, costs);
+    // The GPU partition (identical tasks; the host one for costs it does not take).
     const std::vector<ParallelDataWeighted> tasks =
-        costWeightedTaskPartitioning(csr, costs, result.capacity);
+        costWeightedTaskPartitioning_HIP(csr, costs, result.capacity, queue);
     result.task_count = tasks.size();
 
     const bool large_k = feature_dim > queue.max_work_group_size();

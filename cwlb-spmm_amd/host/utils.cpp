@@ -75,6 +75,32 @@ std::vector<ParallelDataWeighted> costWeightedTaskPartitioning(const CSR_Order& 
     return tasks;
 }
 
+std::vector<ParallelDataWeighted> costWeightedTaskPartitioning_HIP(const CSR_Order& csr,
+                                                                   const SpmmCostParams& costs,
+                                                                   double capacity_weight,
+                                                                   cwlb::Device& q)
+{
+    const int n = static_cast<int>(csr.RowOffset.size()) - 1;
+    if (n <= 0) return {};
+    cwlb::host::CurrentDevice cur(q);
+    DeviceArray<int> rp(csr.RowOffset.size());
+    rp.upload(csr.RowOffset);
+    const cwlb_cost_params c = cwlb::host::to_c(costs);
+    int64_t count = 0;
+    cwlb_status st = cwlb_partition_device(q.ctx(), rp.get(), n, &c, capacity_weight, nullptr, 0,
+                                           &count);
+    if (st == CWLB_UNSUPPORTED) return costWeightedTaskPartitioning(csr, costs, capacity_weight);
+    if (st != CWLB_OK && st != CWLB_INSUFFICIENT) cwlb::throw_status(st, "costWeightedTaskPartitioning_HIP");
+    std::vector<ParallelDataWeighted> tasks(static_cast<std::size_t>(count));
+    if (count == 0) return tasks;
+    DeviceArray<cwlb_task> out(static_cast<std::size_t>(count));
+    cwlb::check(cwlb_partition_device(q.ctx(), rp.get(), n, &c, capacity_weight, out.get(), count,
+                                      &count),
+                "costWeightedTaskPartitioning_HIP");
+    out.download(reinterpret_cast<cwlb_task*>(tasks.data()), tasks.size());
+    return tasks;
+}
+
 bool save_costs_one_per_line(SpmmCostParams costs, const std::string& filepath, bool append,
                              int precision)
 {

@@ -70,7 +70,8 @@ struct SingleSResult {
     Defined::RowMajorMatrixXf output;
 };
 
-// Builds the tasks for S, then runs LOOPCOUNT SpMM launches (the first
+// Builds the tasks for S (on the GPU, identical to the host partition), then
+// runs LOOPCOUNT SpMM launches (the first
 // WARMUPCOUNT untimed) and averages the kernel times of the rest, printing
 // one line per launch (main.cpp:338-412).  The kernel is the large-K form
 // when K exceeds the device's maximum work-group size.  The reordered CSR

@@ -76,6 +76,15 @@ std::vector<ParallelDataWeighted> costWeightedTaskPartitioning(const CSR_Order& 
                                                                const SpmmCostParams& costs,
                                                                double capacity_weight);
 
+// The same partition computed on the GPU (cwlb_partition_device): the
+// RowOffset array is copied to the device, the task list back.  Costs under
+// which a task's row count has no bound (see include/cwlb.h) are partitioned
+// on the host instead; the result is identical either way.
+std::vector<ParallelDataWeighted> costWeightedTaskPartitioning_HIP(const CSR_Order& csr,
+                                                                   const SpmmCostParams& costs,
+                                                                   double capacity_weight,
+                                                                   cwlb::Device& q);
+
 // Cost-file order: compute, load, store, atomic; one per line, fixed
 // notation (reference src/utils.cpp:1024-1092).  Both return false on any
 // failure instead of throwing.

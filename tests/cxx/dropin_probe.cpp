@@ -29,6 +29,7 @@
 //   posarg TEXT                        positive_search_argument
 //   costs-save PATH APPEND PREC CC CL CS CA / costs-read PATH
 //   device                             cwlb::Device properties
+//   partition-gpu ORDER CC CL CS CA S OUT    costWeightedTaskPartitioning_HIP
 //   partition-emul ORDER CC CL CS CA S OUT   the GPU partition's algorithm
 //                                      (fresh-node transitions, pointer doubling,
 //                                      chain expansion) run on the host
@@ -265,6 +266,16 @@ int run(int argc, char** argv)
         const SpmmCostParams c = costs_from(argv + 3);
         const double cap = capacity_from_s(std::stoi(argv[7]), c);
         const std::vector<ParallelDataWeighted> t = costWeightedTaskPartitioning(o, c, cap);
+        Writer w(argv[8]);
+        w.one(cap);
+        w.put(t);
+    } else if (cmd == "partition-gpu") {
+        need(7);
+        const CSR_Order o = read_order(argv[2]);
+        const SpmmCostParams c = costs_from(argv + 3);
+        const double cap = capacity_from_s(std::stoi(argv[7]), c);
+        cwlb::Device q(0);
+        const std::vector<ParallelDataWeighted> t = costWeightedTaskPartitioning_HIP(o, c, cap, q);
         Writer w(argv[8]);
         w.one(cap);
         w.put(t);

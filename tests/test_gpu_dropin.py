@@ -386,3 +386,18 @@ def test_device_partition_edge_cases(gpu_ctx):
         with pytest.raises(capi.CwlbError) as e:
             gpu_ctx.partition_device_count(dev(rp), 50, costs, capi.capacity_from_s(4, costs))
         assert e.value.status == capi.UNSUPPORTED
+
+
+@pytest.mark.parametrize("costs", [SKEWED_COSTS, (0.25, 0.75, 0.0, 0.5)], ids=["gpu", "host"])
+def test_dropin_partition_hip(tmp_path, costs):
+    """costWeightedTaskPartitioning_HIP: identical tasks, on the GPU or (for
+    costs with C_store = 0) through the host partition."""
+    g = workloads.small(4, seed=5)
+    order = oracle.reorder_by_degree(g.row_ptr, g.col_idx, g.val)
+    write_order(tmp_path / "ord", *order)
+    for S in (1, 7, 40):
+        probe("partition-gpu", tmp_path / "ord", *costs, S, tmp_path / "tasks")
+        raw = open(tmp_path / "tasks", "rb").read()
+        got = np.frombuffer(raw[8:], np.int32).reshape(-1, 4)
+        cap = oracle.capacity_from_s(S, costs)
+        assert np.array_equal(got, oracle.partition(order[1], costs, cap))
