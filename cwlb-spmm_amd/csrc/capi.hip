@@ -45,6 +45,17 @@ cwlb_status check_spmm_args(cwlb_ctx* ctx, const SpmmArgs& a)
     return CWLB_OK;
 }
 
+// Reads the status word the last aggregation left (the stream must be idle).
+cwlb_status read_status(cwlb_ctx* ctx)
+{
+    int st = 0;
+    CWLB_HIP_TRY(hipMemcpyAsync(&st, ctx->d_status, sizeof(int), hipMemcpyDeviceToHost, ctx->stream));
+    CWLB_HIP_TRY(hipStreamSynchronize(ctx->stream));
+    if (st & 1) return fail(CWLB_INVALID_ARG, "spmm: a column index is outside [0, h_rows)");
+    if (st & 2) return fail(CWLB_INVALID_ARG, "spmm: an origin entry is outside [0, n_rows)");
+    return CWLB_OK;
+}
+
 cwlb_status finish_timed(cwlb_ctx* ctx, cwlb_timing* timing)
 {
     CWLB_HIP_TRY(hipEventSynchronize(ctx->ev[2]));
@@ -54,11 +65,7 @@ cwlb_status finish_timed(cwlb_ctx* ctx, cwlb_timing* timing)
     timing->zero_us = z * 1000.0f;
     timing->main_us = m * 1000.0f;
     timing->total_us = (z + m) * 1000.0f;
-    int st = 0;
-    CWLB_HIP_TRY(hipMemcpy(&st, ctx->d_status, sizeof(int), hipMemcpyDeviceToHost));
-    if (st & 1) return fail(CWLB_INVALID_ARG, "spmm: a column index is outside [0, h_rows)");
-    if (st & 2) return fail(CWLB_INVALID_ARG, "spmm: an origin entry is outside [0, n_rows)");
-    return CWLB_OK;
+    return read_status(ctx);
 }
 
 cwlb_status run_spmm(cwlb_ctx* ctx, const SpmmArgs& a, uint32_t flags, cwlb_timing* timing)
@@ -173,7 +180,7 @@ cwlb_status cwlb_ctx_synchronize(cwlb_ctx* ctx)
     if (!ctx) return fail(CWLB_INVALID_ARG, "null context");
     DeviceGuard g(ctx->device);
     CWLB_HIP_TRY(hipStreamSynchronize(ctx->stream));
-    return CWLB_OK;
+    return read_status(ctx);
 }
 
 cwlb_status cwlb_ctx_device_info(cwlb_ctx* ctx, cwlb_device_info* out)

@@ -24,11 +24,14 @@ namespace {
 constexpr int kBlock = 256;
 constexpr int kLaneRowMax = 16;
 
-// status bit 0: an offset outside [0, nnz] or a decreasing pair.
+// status bit 0: an offset outside [0, nnz] or a decreasing pair.  Each
+// block writes its maximum degree to block_max[blockIdx.x] (one contended
+// atomic per wave costs milliseconds at 16M rows).
 __global__ void __launch_bounds__(kBlock)
 degree_keys(const int* __restrict__ rp, int n, long long nnz, unsigned* __restrict__ deg,
-            int* __restrict__ status, unsigned* __restrict__ max_deg)
+            int* __restrict__ status, unsigned* __restrict__ block_max)
 {
+    __shared__ unsigned wave_max[kBlock / 64];
     const int i = blockIdx.x * kBlock + threadIdx.x;
     unsigned d = 0;
     if (i < n) {
@@ -41,10 +44,36 @@ degree_keys(const int* __restrict__ rp, int n, long long nnz, unsigned* __restri
         }
         deg[i] = d;
     }
-    // Wave maximum, then one atomic per wave.
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) d = max(d, static_cast<unsigned>(__shfl_xor(static_cast<int>(d), off)));
-    if ((threadIdx.x & 63) == 0 && d > 0) atomicMax(max_deg, d);
+    for (int off = 32; off > 0; off >>= 1)
+        d = max(d, static_cast<unsigned>(__shfl_xor(static_cast<int>(d), off)));
+    if ((threadIdx.x & 63) == 0) wave_max[threadIdx.x >> 6] = d;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        unsigned m = 0;
+#pragma unroll
+        for (int w = 0; w < kBlock / 64; ++w) m = max(m, wave_max[w]);
+        block_max[blockIdx.x] = m;
+    }
+}
+
+// One block: the maximum of the per-block maxima into *out.
+__global__ void __launch_bounds__(1024)
+reduce_max(const unsigned* __restrict__ v, long long n, unsigned* __restrict__ out)
+{
+    __shared__ unsigned part[1024 / 64];
+    unsigned m = 0;
+    for (long long i = threadIdx.x; i < n; i += 1024) m = max(m, v[i]);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1)
+        m = max(m, static_cast<unsigned>(__shfl_xor(static_cast<int>(m), off)));
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = m;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        unsigned r = 0;
+        for (int w = 0; w < 1024 / 64; ++w) r = max(r, part[w]);
+        *out = r;
+    }
 }
 
 __global__ void __launch_bounds__(kBlock)
@@ -186,19 +215,24 @@ cwlb_status launch_reorder(cwlb_ctx* ctx, int32_t n, int64_t nnz, const int32_t*
         return fail(CWLB_INVALID_ARG, "reorder: null device pointer");
 
     const size_t un = static_cast<size_t>(n);
-    DevMem keys, keys_sorted, flags;
+    const unsigned grid = static_cast<unsigned>((un + kBlock - 1) / kBlock);
+    DevMem keys, keys_sorted, flags, bmax;
     CWLB_HIP_TRY(keys.alloc(sizeof(unsigned) * un));
     CWLB_HIP_TRY(keys_sorted.alloc(sizeof(unsigned) * un));
     CWLB_HIP_TRY(flags.alloc(2 * sizeof(int)));
+    CWLB_HIP_TRY(bmax.alloc(sizeof(unsigned) * grid));
     auto* d_keys = static_cast<unsigned*>(keys.p);
     auto* d_sorted = static_cast<unsigned*>(keys_sorted.p);
     auto* d_status = static_cast<int*>(flags.p);
     auto* d_max = reinterpret_cast<unsigned*>(d_status + 1);
     CWLB_HIP_TRY(hipMemsetAsync(d_status, 0, 2 * sizeof(int), st));
-    const unsigned grid = static_cast<unsigned>((un + kBlock - 1) / kBlock);
     hipLaunchKernelGGL(degree_keys, dim3(grid), dim3(kBlock), 0, st, rp, n,
-                       static_cast<long long>(nnz), d_keys, d_status, d_max);
-    CWLB_HIP_TRY(hipGetLastError());
+                       static_cast<long long>(nnz), d_keys, d_status,
+                       static_cast<unsigned*>(bmax.p));
+    CWLB_LAUNCH_CHECK("degree_keys");
+    hipLaunchKernelGGL(reduce_max, dim3(1), dim3(1024), 0, st, static_cast<unsigned*>(bmax.p),
+                       static_cast<long long>(grid), d_max);
+    CWLB_LAUNCH_CHECK("reduce_max");
     int host_flags[2] = {0, 0};
     int ends[2] = {0, 0};
     CWLB_HIP_TRY(hipMemcpyAsync(host_flags, d_status, sizeof host_flags, hipMemcpyDeviceToHost, st));

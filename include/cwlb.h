@@ -97,6 +97,9 @@ const char* cwlb_last_error(void);
 cwlb_status cwlb_ctx_create(int device, void* stream, cwlb_ctx** out);
 cwlb_status cwlb_ctx_destroy(cwlb_ctx* ctx);
 cwlb_status cwlb_ctx_set_stream(cwlb_ctx* ctx, void* stream);
+/* Waits for the context's stream; then reports, as CWLB_INVALID_ARG, a bad
+ * column index or origin entry that the last aggregation met (asynchronous
+ * calls cannot report it themselves). */
 cwlb_status cwlb_ctx_synchronize(cwlb_ctx* ctx);
 cwlb_status cwlb_ctx_device_info(cwlb_ctx* ctx, cwlb_device_info* out);
 /* Schedule of later SpMM calls on this context: tasks executed per wave
@@ -140,7 +143,11 @@ cwlb_status cwlb_ctx_set_locality(cwlb_ctx* ctx, int32_t run_order, int32_t xcd_
  * K == 0 or n_tasks == 0: C is cleared (when CWLB_SPMM_ZERO_OUTPUT is set)
  * and timings are 0, as the reference returns a zero matrix with time 0
  * (parallelMatrix.cpp:80-83, 101-104).
- * timing may be NULL (asynchronous); otherwise the call synchronises.
+ * timing may be NULL (asynchronous: bad column indices or origin entries
+ * are then reported by the next cwlb_ctx_synchronize); otherwise the call
+ * synchronises.  The default and CWLB_SPMM_ZERO_OUTPUT paths launch kernels
+ * only (no memset nodes, no allocation), so an asynchronous call can be
+ * captured into a HIP graph; run_order = 2 (cwlb_ctx_set_locality) cannot.
  *
  * cwlb_spmm_mean_f32 mirrors spmmKernel: K > max work-group size (1024)
  * returns CWLB_INVALID_ARG (parallelMatrix.cpp:84-88).

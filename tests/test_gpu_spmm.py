@@ -471,3 +471,59 @@ def test_full_config_locality_modes_agree(gpu_ctx, cfg):
     finally:
         gpu_ctx.set_schedule(0, 0)
         gpu_ctx.set_locality(0, 0)
+
+
+def test_async_call_reports_bad_column_at_synchronize(gpu_ctx):
+    g = workloads.small(1, seed=2)
+    H = synth.features(g.n, 32, 3)
+    p = problem(g, UNIT_COSTS, 6)
+    ci = p.col_idx.copy()
+    ci[len(ci) // 3] = -4
+    torch = torch_mod()
+    d = [dev(x) for x in (p.row_ptr, ci, p.val, p.origin)]
+    d_t = dev(np.ascontiguousarray(p.tasks, np.int32).reshape(-1))
+    C = torch.zeros((g.n, 32), dtype=torch.float32, device="cuda")
+    gpu_ctx.spmm(*d, g.n, g.nnz, dev(H), g.n, 32, d_t, len(p.tasks), C, timed=False)
+    with pytest.raises(capi.CwlbError) as e:
+        gpu_ctx.synchronize()
+    assert e.value.status == capi.INVALID_ARG
+    # a good call clears the status word
+    d[1] = dev(p.col_idx)
+    gpu_ctx.spmm(*d, g.n, g.nnz, dev(H), g.n, 32, d_t, len(p.tasks), C, timed=False)
+    gpu_ctx.synchronize()
+
+
+@pytest.mark.parametrize("flags", [0, capi.ZERO_OUTPUT], ids=["default", "zero_output"])
+def test_hip_graph_capture_and_replay(gpu_ctx, flags):
+    """An asynchronous call captured into a HIP graph (torch.cuda.CUDAGraph)
+    and replayed several times, with eager work and synchronisations in
+    between, gives the eager result on every replay."""
+    torch = torch_mod()
+    g = workloads.small(4, seed=21)
+    K = 64
+    p = problem(g, SKEWED_COSTS, 9)
+    d_rp, d_ci, d_v, d_o = dev(p.row_ptr), dev(p.col_idx), dev(p.val), dev(p.origin)
+    d_t = dev(np.ascontiguousarray(p.tasks, np.int32).reshape(-1))
+    H = dev(synth.features(g.n, K, 4))
+    C = torch.zeros((g.n, K), dtype=torch.float32, device="cuda")
+    gpu_ctx.spmm(d_rp, d_ci, d_v, d_o, g.n, g.nnz, H, g.n, K, d_t, len(p.tasks), C, flags=flags)
+    eager = C.clone()
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        gpu_ctx.set_stream(side.cuda_stream)
+        with torch.cuda.graph(graph, stream=side):
+            gpu_ctx.spmm(d_rp, d_ci, d_v, d_o, g.n, g.nnz, H, g.n, K, d_t, len(p.tasks), C,
+                         flags=flags, timed=False)
+    gpu_ctx.set_stream(torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    for i in range(4):
+        C.fill_(float("nan") if flags else float(i))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        np.testing.assert_allclose(C.cpu().numpy(), eager.cpu().numpy(), rtol=RTOL, atol=ATOL)
+        _ = (H * 2.0).sum().item()  # eager work between replays
+    ref32 = oracle.spmm_mean_f32(p.row_ptr, p.col_idx, p.val, p.origin, H.cpu().numpy(), p.tasks)
+    np.testing.assert_allclose(C.cpu().numpy(), ref32, rtol=RTOL, atol=ATOL)
