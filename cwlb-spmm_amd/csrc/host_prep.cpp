@@ -219,6 +219,7 @@ cwlb_status cwlb_reorder_by_degree(int32_t n_rows, int64_t nnz, const int32_t* r
     for (int32_t r = 0; r < n_rows; ++r) {
         const int32_t o = origin[r];
         const int32_t len = row_ptr[o + 1] - row_ptr[o];
+        if (len == 0) continue;  // the arrays may be null when nnz == 0
         std::memcpy(col_idx_out + row_ptr_out[r], col_idx + row_ptr[o],
                     sizeof(int32_t) * static_cast<size_t>(len));
         std::memcpy(val_out + row_ptr_out[r], val + row_ptr[o], sizeof(float) * static_cast<size_t>(len));
