@@ -29,18 +29,24 @@ sys.path.insert(0, os.path.join(ROOT, "cwlb-spmm_amd"))
 METRIC = "SpMM GFLOP/s (2·nnz·K/t) + achieved HBM GB/s vs peak, FP32 mean agg"
 HBM_PEAK_GBS = 8000.0
 COST_FILE = os.path.join(ROOT, "cwlb-spmm_amd", "resources", "spmm_costs_gfx950.txt")
-PMC_SUMMARY = os.path.join(ROOT, "profiles", "spmm_mean_runs_rmat22_k128_pmc.txt")
+# Committed rocprofv3 PMC summaries per workload configuration (traffic per
+# aggregation launch, FETCH_SIZE + WRITE_SIZE scaled by a known-size copy).
+PMC_SUMMARY = {
+    4: os.path.join(ROOT, "profiles", "spmm_mean_runs_rmat22_k128_pmc.txt"),
+    5: os.path.join(ROOT, "profiles", "spmm_mean_runs_mesh16m_k32_trace_pmc.md"),
+    3: os.path.join(ROOT, "profiles", "spmm_mean_runs_sbm240k_k600_trace_pmc.md"),
+}
 
 
 def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def measured_traffic():
+def measured_traffic(cfg):
     """HBM bytes per aggregation launch from the committed rocprofv3 PMC summary."""
     try:
-        text = open(PMC_SUMMARY).read()
-    except OSError:
+        text = open(PMC_SUMMARY[cfg]).read()
+    except (KeyError, OSError):
         return None
     m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", text)
     return float(m.group(1)) if m else None
@@ -98,6 +104,11 @@ def main():
     ap.add_argument("--s", type=int, default=0, help="fixed segment size (0 = best candidate)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--tasks-per-wave", type=int, default=0,
+                    help="fixed launch schedule (with --slices) instead of tuning")
+    ap.add_argument("--slices", type=int, default=0)
+    ap.add_argument("--no-tune", action="store_true",
+                    help="keep the automatic launch schedule (no cwlb_ctx_tune_schedule)")
     ap.add_argument("--no-host-call", action="store_true",
                     help="skip the one host-pointer call (inputs copied in, C copied out)")
     ap.add_argument("--costs", default=COST_FILE, help="cost file (four coefficients)")
@@ -156,10 +167,24 @@ def main():
         log(f"candidate S={S}: tasks={len(tk)} mean {us:.1f} us")
         if best is None or us < best[1]:
             best = (S, us, tk, d_t)
-    S, _, tasks, d_t = best
+    S, auto_us, tasks, d_t = best
     T = len(tasks)
     prep = preprocessing_times(ctx, g, rp, costs, S, tasks, reorder_host_ms)
     log(f"preprocessing: {prep}")
+    # Launch schedule for this graph and S: measured once, like the S search
+    # (cwlb_ctx_tune_schedule; 0, 0 = the automatic choice won).
+    schedule = {"tasks_per_wave": 0, "feature_slices": 0, "tuned": False,
+                "automatic_schedule_us": round(float(auto_us), 1)}
+    if args.tasks_per_wave or args.slices:
+        ctx.set_schedule(args.tasks_per_wave, args.slices)
+        schedule.update(tasks_per_wave=args.tasks_per_wave, feature_slices=args.slices)
+        log(f"fixed schedule: tasks_per_wave={args.tasks_per_wave} feature_slices={args.slices}")
+    elif not args.no_tune:
+        t0 = time.perf_counter()
+        m, sl = ctx.tune_schedule(d_rp, d_ci, d_v, d_o, g.n, g.nnz, H, g.n, K, d_t, T, C, trials=3)
+        schedule.update(tasks_per_wave=m, feature_slices=sl, tuned=True,
+                        tuning_ms=round((time.perf_counter() - t0) * 1e3, 1))
+        log(f"tuned schedule: tasks_per_wave={m} feature_slices={sl}")
 
     # Timed region: W warm-ups, K steps, synchronised on both sides.
     for _ in range(args.warmup):
@@ -208,7 +233,7 @@ def main():
     gflops = flops / (ms_per_step * 1e-3) / 1e9
     b_alg = workloads.algorithmic_bytes(g.n, g.nnz, K, T)
     achieved = b_alg / (main_us * 1e-6) / 1e9
-    traffic = measured_traffic()
+    traffic = measured_traffic(cfg)
 
     cpu = None
     if not args.no_cpu:
@@ -257,6 +282,7 @@ def main():
                    "per_task_mode_us": round(per_task_us, 2),
                    "host_pointer_call_ms": None if host_call_ms is None else round(host_call_ms, 1),
                    "preprocessing": prep,
+                   "schedule": schedule,
                    "algorithmic_bytes": b_alg},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),

@@ -1,4 +1,5 @@
 // C ABI of libcwlb: contexts, errors and the SpMM entry points.
+#include <algorithm>
 #include <cstdio>
 #include <cstring>
 #include <string>
@@ -236,6 +237,56 @@ cwlb_status cwlb_spmm_mean_f32(cwlb_ctx* ctx, const int32_t* row_ptr, const int3
                     "use spmmKernelLargeKFallback for larger K.");
     SpmmArgs a{row_ptr, col_idx, val, origin, n_rows, nnz, H, h_rows, K, tasks, n_tasks, C};
     return run_spmm(ctx, a, flags, timing);
+}
+
+cwlb_status cwlb_ctx_tune_schedule(cwlb_ctx* ctx, const int32_t* row_ptr, const int32_t* col_idx,
+                                   const float* val, const int32_t* origin, int32_t n_rows,
+                                   int64_t nnz, const float* H, int64_t h_rows, int32_t K,
+                                   const cwlb_task* tasks, int64_t n_tasks, float* C,
+                                   int32_t trials, int32_t* tasks_per_wave_out,
+                                   int32_t* feature_slices_out)
+{
+    if (!ctx) return fail(CWLB_INVALID_ARG, "null context");
+    if (trials <= 0) return fail(CWLB_INVALID_ARG, "cwlb_ctx_tune_schedule: trials must be positive");
+    SpmmArgs a{row_ptr, col_idx, val, origin, n_rows, nnz, H, h_rows, K, tasks, n_tasks, C};
+    cwlb_status st = check_spmm_args(ctx, a);
+    if (st != CWLB_OK) return st;
+    // Candidates: the automatic choice, then every run length and slice
+    // count the kernel takes for this K.
+    std::vector<std::pair<int, int>> cands{{0, 0}};
+    for (int sl : {1, 2, 4})
+        if (sl == 1 || (K % (4 * sl) == 0 && K / sl >= 32))
+            for (int m : {2, 4, 8, 16, 32, 64}) cands.emplace_back(m, sl);
+    const int keep_m = ctx->sched_tasks_per_wave, keep_sl = ctx->sched_slices;
+    float best_us = 0.0f;
+    std::pair<int, int> best{0, 0};
+    std::vector<float> times(static_cast<size_t>(trials));
+    for (const auto& c : cands) {
+        ctx->sched_tasks_per_wave = c.first;
+        ctx->sched_slices = c.second;
+        st = run_spmm(ctx, a, 0, nullptr);  // warm-up
+        for (int t = 0; st == CWLB_OK && t < trials; ++t) {
+            cwlb_timing tm{};
+            st = run_spmm(ctx, a, 0, &tm);
+            times[static_cast<size_t>(t)] = tm.total_us;
+        }
+        if (st != CWLB_OK) {
+            ctx->sched_tasks_per_wave = keep_m;
+            ctx->sched_slices = keep_sl;
+            return st;
+        }
+        std::sort(times.begin(), times.end());
+        const float med = times[times.size() / 2];
+        if (best_us == 0.0f || med < best_us) {
+            best_us = med;
+            best = c;
+        }
+    }
+    ctx->sched_tasks_per_wave = best.first;
+    ctx->sched_slices = best.second;
+    if (tasks_per_wave_out) *tasks_per_wave_out = best.first;
+    if (feature_slices_out) *feature_slices_out = best.second;
+    return CWLB_OK;
 }
 
 cwlb_status cwlb_spmm_mean_f32_large_k(cwlb_ctx* ctx, const int32_t* row_ptr,

@@ -23,7 +23,7 @@ PER_TASK = 0x2
 EXPORTS = [
     "cwlb_version", "cwlb_last_error", "cwlb_ctx_create", "cwlb_ctx_destroy",
     "cwlb_ctx_set_stream", "cwlb_ctx_synchronize", "cwlb_ctx_device_info", "cwlb_ctx_set_schedule",
-    "cwlb_ctx_set_locality",
+    "cwlb_ctx_set_locality", "cwlb_ctx_tune_schedule",
     "cwlb_spmm_mean_f32", "cwlb_spmm_mean_f32_large_k", "cwlb_spmm_mean_f32_host",
     "cwlb_reorder_by_degree", "cwlb_reorder_by_degree_device", "cwlb_partition",
     "cwlb_partition_device",
@@ -99,6 +99,8 @@ def lib():
         L.cwlb_ctx_device_info.argtypes = [vp, C.POINTER(DeviceInfo)]
         L.cwlb_ctx_set_schedule.argtypes = [vp, i32, i32]
         L.cwlb_ctx_set_locality.argtypes = [vp, i32, i32]
+        L.cwlb_ctx_tune_schedule.argtypes = [vp, vp, vp, vp, vp, i32, i64, vp, i64, i32, vp, i64,
+                                             vp, i32, C.POINTER(i32), C.POINTER(i32)]
         spmm = [vp, vp, vp, vp, vp, i32, i64, vp, i64, i32, vp, i64, vp, u32, C.POINTER(Timing)]
         L.cwlb_spmm_mean_f32.argtypes = spmm
         L.cwlb_spmm_mean_f32_large_k.argtypes = spmm
@@ -263,6 +265,16 @@ class Context:
 
     def set_locality(self, run_order=0, xcd_blocks=0):
         check(lib().cwlb_ctx_set_locality(self.h, int(run_order), int(xcd_blocks)))
+
+    def tune_schedule(self, row_ptr, col_idx, val, origin, n_rows, nnz, H, h_rows, K, tasks,
+                      n_tasks, C_out, trials=3):
+        """cwlb_ctx_tune_schedule: sets and returns the fastest (tasks_per_wave, slices)."""
+        m, sl = i32(), i32()
+        check(lib().cwlb_ctx_tune_schedule(self.h, _ptr(row_ptr), _ptr(col_idx), _ptr(val),
+                                           _ptr(origin), int(n_rows), int(nnz), _ptr(H),
+                                           int(h_rows), int(K), _ptr(tasks), int(n_tasks),
+                                           _ptr(C_out), int(trials), C.byref(m), C.byref(sl)))
+        return m.value, sl.value
 
     def synchronize(self):
         check(lib().cwlb_ctx_synchronize(self.h))

@@ -176,6 +176,22 @@ cwlb_status cwlb_spmm_mean_f32_large_k(cwlb_ctx* ctx, const int32_t* row_ptr,
                                        const cwlb_task* tasks, int64_t n_tasks, float* C,
                                        uint32_t flags, cwlb_timing* timing);
 
+/* Times the aggregation of these (device) inputs under the automatic
+ * schedule and under every tasks-per-wave value in {2, 4, ..., 64} with 1, 2
+ * or 4 feature slices (where K allows them), `trials` event-timed calls each
+ * after one warm-up (median of split-row clearing + aggregation), and sets
+ * the fastest on the context (cwlb_ctx_set_schedule); the choice is also
+ * returned through the two optional out pointers (0, 0 = the automatic
+ * schedule won).  C receives the result.  Synchronises.  No counterpart in
+ * the reference, whose one task per work-group has nothing to tune; like
+ * its S search, it is meant to run once per graph before timed runs. */
+cwlb_status cwlb_ctx_tune_schedule(cwlb_ctx* ctx, const int32_t* row_ptr, const int32_t* col_idx,
+                                   const float* val, const int32_t* origin, int32_t n_rows,
+                                   int64_t nnz, const float* H, int64_t h_rows, int32_t K,
+                                   const cwlb_task* tasks, int64_t n_tasks, float* C,
+                                   int32_t trials, int32_t* tasks_per_wave_out,
+                                   int32_t* feature_slices_out);
+
 /* Host-pointer form: copies the inputs to the device, runs the call, copies
  * C back (the reference's per-call sycl::buffer behaviour,
  * parallelMatrix.cpp:115-121).  C is always cleared first.  Dispatches on K

@@ -527,3 +527,33 @@ def test_hip_graph_capture_and_replay(gpu_ctx, flags):
         _ = (H * 2.0).sum().item()  # eager work between replays
     ref32 = oracle.spmm_mean_f32(p.row_ptr, p.col_idx, p.val, p.origin, H.cpu().numpy(), p.tasks)
     np.testing.assert_allclose(C.cpu().numpy(), ref32, rtol=RTOL, atol=ATOL)
+
+
+def test_tune_schedule(gpu_ctx):
+    """cwlb_ctx_tune_schedule picks one of its candidates, leaves it on the
+    context, and every schedule it tried computes the same result."""
+    g = workloads.small(4, seed=13)
+    K = 128
+    p = problem(g, SKEWED_COSTS, 16)
+    H = synth.features(g.n, K, 2)
+    torch = torch_mod()
+    d_rp, d_ci, d_v, d_o = dev(p.row_ptr), dev(p.col_idx), dev(p.val), dev(p.origin)
+    d_t = dev(np.ascontiguousarray(p.tasks, np.int32).reshape(-1))
+    d_H = dev(H)
+    C = torch.full((g.n, K), float("nan"), dtype=torch.float32, device="cuda")
+    try:
+        m, sl = gpu_ctx.tune_schedule(d_rp, d_ci, d_v, d_o, g.n, g.nnz, d_H, g.n, K, d_t,
+                                      len(p.tasks), C, trials=2)
+        assert (m, sl) == (0, 0) or (m in (2, 4, 8, 16, 32, 64) and sl in (1, 2, 4))
+        ref32, ref64 = oracle_pair(p, g, H)
+        check(C.cpu().numpy(), ref32)
+        C.fill_(float("nan"))
+        gpu_ctx.spmm(d_rp, d_ci, d_v, d_o, g.n, g.nnz, d_H, g.n, K, d_t, len(p.tasks), C)
+        check(C.cpu().numpy(), ref32)
+        check(C.cpu().numpy(), ref64)
+        with pytest.raises(capi.CwlbError) as e:
+            gpu_ctx.tune_schedule(d_rp, d_ci, d_v, d_o, g.n, g.nnz, d_H, g.n, K, d_t,
+                                  len(p.tasks), C, trials=0)
+        assert e.value.status == capi.INVALID_ARG
+    finally:
+        gpu_ctx.set_schedule(0, 0)
