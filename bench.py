@@ -107,6 +107,10 @@ def main():
     ap.add_argument("--tasks-per-wave", type=int, default=0,
                     help="fixed launch schedule (with --slices) instead of tuning")
     ap.add_argument("--slices", type=int, default=0)
+    ap.add_argument("--run-order", type=int, default=0,
+                    help="fixed run order (cwlb_ctx_set_locality: 1 task order, 2 by output row)")
+    ap.add_argument("--xcd-blocks", type=int, default=0,
+                    help="fixed XCD placement (1 interleaved, 2 contiguous)")
     ap.add_argument("--no-tune", action="store_true",
                     help="keep the automatic launch schedule (no cwlb_ctx_tune_schedule)")
     ap.add_argument("--no-host-call", action="store_true",
@@ -175,16 +179,19 @@ def main():
     # (cwlb_ctx_tune_schedule; 0, 0 = the automatic choice won).
     schedule = {"tasks_per_wave": 0, "feature_slices": 0, "tuned": False,
                 "automatic_schedule_us": round(float(auto_us), 1)}
-    if args.tasks_per_wave or args.slices:
+    if args.tasks_per_wave or args.slices or args.run_order or args.xcd_blocks:
         ctx.set_schedule(args.tasks_per_wave, args.slices)
-        schedule.update(tasks_per_wave=args.tasks_per_wave, feature_slices=args.slices)
-        log(f"fixed schedule: tasks_per_wave={args.tasks_per_wave} feature_slices={args.slices}")
+        ctx.set_locality(args.run_order, args.xcd_blocks)
+        schedule.update(tasks_per_wave=args.tasks_per_wave, feature_slices=args.slices,
+                        run_order=args.run_order, xcd_blocks=args.xcd_blocks)
+        log(f"fixed schedule: {schedule}")
     elif not args.no_tune:
         t0 = time.perf_counter()
-        m, sl = ctx.tune_schedule(d_rp, d_ci, d_v, d_o, g.n, g.nnz, H, g.n, K, d_t, T, C, trials=3)
-        schedule.update(tasks_per_wave=m, feature_slices=sl, tuned=True,
-                        tuning_ms=round((time.perf_counter() - t0) * 1e3, 1))
-        log(f"tuned schedule: tasks_per_wave={m} feature_slices={sl}")
+        m, sl, (order, xcd) = ctx.tune_schedule(d_rp, d_ci, d_v, d_o, g.n, g.nnz, H, g.n, K, d_t,
+                                                T, C, trials=3, locality=True)
+        schedule.update(tasks_per_wave=m, feature_slices=sl, run_order=order, xcd_blocks=xcd,
+                        tuned=True, tuning_ms=round((time.perf_counter() - t0) * 1e3, 1))
+        log(f"tuned schedule: {schedule}")
 
     # Timed region: W warm-ups, K steps, synchronised on both sides.
     for _ in range(args.warmup):

@@ -222,6 +222,7 @@ cwlb_status cwlb_ctx_set_locality(cwlb_ctx* ctx, int32_t run_order, int32_t xcd_
                                       "(contiguous)");
     ctx->sched_order = run_order;
     ctx->sched_xcd = xcd_blocks;
+    ctx->order_runs = -1;  // recompute the run order at the next call
     return CWLB_OK;
 }
 
@@ -244,7 +245,7 @@ cwlb_status cwlb_ctx_tune_schedule(cwlb_ctx* ctx, const int32_t* row_ptr, const 
                                    int64_t nnz, const float* H, int64_t h_rows, int32_t K,
                                    const cwlb_task* tasks, int64_t n_tasks, float* C,
                                    int32_t trials, int32_t* tasks_per_wave_out,
-                                   int32_t* feature_slices_out)
+                                   int32_t* feature_slices_out, int32_t* locality_out)
 {
     if (!ctx) return fail(CWLB_INVALID_ARG, "null context");
     if (trials <= 0) return fail(CWLB_INVALID_ARG, "cwlb_ctx_tune_schedule: trials must be positive");
@@ -282,8 +283,44 @@ cwlb_status cwlb_ctx_tune_schedule(cwlb_ctx* ctx, const int32_t* row_ptr, const 
             best = c;
         }
     }
+    // Locality placements for the best schedule: runs sorted by output row
+    // (the order is computed once and reused), with interleaved or
+    // contiguous XCD stretches.
+    const int keep_order = ctx->sched_order, keep_xcd = ctx->sched_xcd;
     ctx->sched_tasks_per_wave = best.first;
     ctx->sched_slices = best.second;
+    int best_order = keep_order, best_xcd = keep_xcd;
+    if (locality_out) {
+        for (const auto& loc : {std::pair<int, int>{2, 1}, {2, 2}}) {
+            ctx->sched_order = loc.first;
+            ctx->sched_xcd = loc.second;
+            ctx->order_runs = -1;
+            st = run_spmm(ctx, a, 0, nullptr);  // warm-up, builds the order
+            for (int t = 0; st == CWLB_OK && t < trials; ++t) {
+                cwlb_timing tm{};
+                st = run_spmm(ctx, a, 0, &tm);
+                times[static_cast<size_t>(t)] = tm.total_us;
+            }
+            if (st != CWLB_OK) break;
+            std::sort(times.begin(), times.end());
+            const float med = times[times.size() / 2];
+            if (med < best_us) {
+                best_us = med;
+                best_order = loc.first;
+                best_xcd = loc.second;
+            }
+        }
+        ctx->sched_order = best_order;
+        ctx->sched_xcd = best_xcd;
+        ctx->order_runs = -1;
+        if (st != CWLB_OK) {
+            ctx->sched_order = keep_order;
+            ctx->sched_xcd = keep_xcd;
+            return st;
+        }
+        locality_out[0] = best_order;
+        locality_out[1] = best_xcd;
+    }
     if (tasks_per_wave_out) *tasks_per_wave_out = best.first;
     if (feature_slices_out) *feature_slices_out = best.second;
     return CWLB_OK;

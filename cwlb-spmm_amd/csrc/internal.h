@@ -35,6 +35,14 @@ struct cwlb_ctx {
     unsigned* d_run_keys_sorted = nullptr;
     int* d_run_order = nullptr;
     long long run_cap = 0;
+    // What d_run_order was computed for.  Any permutation of the runs gives
+    // the same result, so an order reused for rewritten task contents only
+    // costs speed; cwlb_ctx_set_locality forgets it.
+    const void* order_tasks = nullptr;
+    const void* order_origin = nullptr;
+    long long order_n_tasks = -1;
+    long long order_runs = -1;
+    int order_M = 0;
     void* d_sort_temp = nullptr;
     size_t sort_temp_bytes = 0;
 };
@@ -96,7 +104,8 @@ cwlb_status launch_spmm_mean(cwlb_ctx* ctx, const SpmmArgs& a, bool zero_all, bo
 
 // Computes into ctx->d_run_order a permutation of the n_runs runs (runs of
 // M tasks) sorted by the original id of each run's first row, on
-// ctx->stream; *order receives ctx->d_run_order.
+// ctx->stream, unless the order of the same task array, origin array, task
+// count and run length is already there; *order receives ctx->d_run_order.
 cwlb_status build_run_order(cwlb_ctx* ctx, const SpmmArgs& a, int M, long long n_runs,
                             const int** order);
 

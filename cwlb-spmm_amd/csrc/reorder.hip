@@ -163,6 +163,12 @@ cwlb_status build_run_order(cwlb_ctx* ctx, const SpmmArgs& a, int M, long long n
         *order = nullptr;
         return CWLB_OK;
     }
+    if (ctx->order_tasks == a.tasks && ctx->order_origin == a.origin &&
+        ctx->order_n_tasks == a.n_tasks && ctx->order_runs == n_runs && ctx->order_M == M) {
+        *order = ctx->d_run_order;
+        return CWLB_OK;
+    }
+    ctx->order_runs = -1;
     if (n_runs > ctx->run_cap) {
         cwlb_status s = grow(&ctx->d_run_keys, 0, n_runs);
         if (s == CWLB_OK) s = grow(&ctx->d_run_keys_sorted, 0, n_runs);
@@ -194,6 +200,11 @@ cwlb_status build_run_order(cwlb_ctx* ctx, const SpmmArgs& a, int M, long long n
     CWLB_HIP_TRY(rocprim::radix_sort_pairs(ctx->d_sort_temp, bytes, ctx->d_run_keys,
                                            ctx->d_run_keys_sorted, ids, ctx->d_run_order, n_runs,
                                            0u, end_bit, st));
+    ctx->order_tasks = a.tasks;
+    ctx->order_origin = a.origin;
+    ctx->order_n_tasks = a.n_tasks;
+    ctx->order_runs = n_runs;
+    ctx->order_M = M;
     *order = ctx->d_run_order;
     return CWLB_OK;
 }

@@ -100,7 +100,7 @@ def lib():
         L.cwlb_ctx_set_schedule.argtypes = [vp, i32, i32]
         L.cwlb_ctx_set_locality.argtypes = [vp, i32, i32]
         L.cwlb_ctx_tune_schedule.argtypes = [vp, vp, vp, vp, vp, i32, i64, vp, i64, i32, vp, i64,
-                                             vp, i32, C.POINTER(i32), C.POINTER(i32)]
+                                             vp, i32, C.POINTER(i32), C.POINTER(i32), vp]
         spmm = [vp, vp, vp, vp, vp, i32, i64, vp, i64, i32, vp, i64, vp, u32, C.POINTER(Timing)]
         L.cwlb_spmm_mean_f32.argtypes = spmm
         L.cwlb_spmm_mean_f32_large_k.argtypes = spmm
@@ -267,13 +267,18 @@ class Context:
         check(lib().cwlb_ctx_set_locality(self.h, int(run_order), int(xcd_blocks)))
 
     def tune_schedule(self, row_ptr, col_idx, val, origin, n_rows, nnz, H, h_rows, K, tasks,
-                      n_tasks, C_out, trials=3):
-        """cwlb_ctx_tune_schedule: sets and returns the fastest (tasks_per_wave, slices)."""
+                      n_tasks, C_out, trials=3, locality=False):
+        """cwlb_ctx_tune_schedule: sets and returns the fastest (tasks_per_wave, slices), and
+        with locality=True also (run_order, xcd_blocks) as a third element."""
         m, sl = i32(), i32()
+        loc = np.zeros(2, np.int32)
         check(lib().cwlb_ctx_tune_schedule(self.h, _ptr(row_ptr), _ptr(col_idx), _ptr(val),
                                            _ptr(origin), int(n_rows), int(nnz), _ptr(H),
                                            int(h_rows), int(K), _ptr(tasks), int(n_tasks),
-                                           _ptr(C_out), int(trials), C.byref(m), C.byref(sl)))
+                                           _ptr(C_out), int(trials), C.byref(m), C.byref(sl),
+                                           loc.ctypes.data if locality else None))
+        if locality:
+            return m.value, sl.value, (int(loc[0]), int(loc[1]))
         return m.value, sl.value
 
     def synchronize(self):

@@ -113,8 +113,11 @@ cwlb_status cwlb_ctx_set_schedule(cwlb_ctx* ctx, int32_t tasks_per_wave, int32_t
 
 /* Locality of later SpMM calls on this context.  run_order: 0 automatic,
  * 1 runs in task order, 2 runs sorted by the original id of their first row
- * (computed on the device at each call; groups the rows of all degree
- * classes that neighbour each other in the original numbering).
+ * (a device sort, redone only when the task array, origin array, task count
+ * or run length changes; it groups the rows of all degree classes that
+ * neighbour each other in the original numbering.  Every order of the runs
+ * gives the same result, so after rewriting a task array in place only the
+ * speed can suffer; calling this function again forces a new sort).
  * xcd_blocks: 0 automatic, 1 consecutive run blocks interleaved over the 8
  * XCDs, 2 each XCD takes one contiguous stretch of run blocks.  Ignored with
  * CWLB_SPMM_PER_TASK.  No counterpart in the reference; tuning and tests use
@@ -181,16 +184,20 @@ cwlb_status cwlb_spmm_mean_f32_large_k(cwlb_ctx* ctx, const int32_t* row_ptr,
  * or 4 feature slices (where K allows them), `trials` event-timed calls each
  * after one warm-up (median of split-row clearing + aggregation), and sets
  * the fastest on the context (cwlb_ctx_set_schedule); the choice is also
- * returned through the two optional out pointers (0, 0 = the automatic
- * schedule won).  C receives the result.  Synchronises.  No counterpart in
- * the reference, whose one task per work-group has nothing to tune; like
- * its S search, it is meant to run once per graph before timed runs. */
+ * returned through the optional out pointers (0, 0 = the automatic schedule
+ * won).  With locality_out non-null (two int32), the fastest schedule is
+ * also timed with runs sorted by output row (interleaved and contiguous XCD
+ * placement, cwlb_ctx_set_locality), the winner is kept on the context and
+ * written there (1, 0 or the context's previous setting = task order kept).
+ * C receives the result.  Synchronises.  No counterpart in the reference,
+ * whose one task per work-group has nothing to tune; like its S search, it
+ * is meant to run once per graph before timed runs. */
 cwlb_status cwlb_ctx_tune_schedule(cwlb_ctx* ctx, const int32_t* row_ptr, const int32_t* col_idx,
                                    const float* val, const int32_t* origin, int32_t n_rows,
                                    int64_t nnz, const float* H, int64_t h_rows, int32_t K,
                                    const cwlb_task* tasks, int64_t n_tasks, float* C,
                                    int32_t trials, int32_t* tasks_per_wave_out,
-                                   int32_t* feature_slices_out);
+                                   int32_t* feature_slices_out, int32_t* locality_out);
 
 /* Host-pointer form: copies the inputs to the device, runs the call, copies
  * C back (the reference's per-call sycl::buffer behaviour,

@@ -542,9 +542,10 @@ def test_tune_schedule(gpu_ctx):
     d_H = dev(H)
     C = torch.full((g.n, K), float("nan"), dtype=torch.float32, device="cuda")
     try:
-        m, sl = gpu_ctx.tune_schedule(d_rp, d_ci, d_v, d_o, g.n, g.nnz, d_H, g.n, K, d_t,
-                                      len(p.tasks), C, trials=2)
+        m, sl, loc = gpu_ctx.tune_schedule(d_rp, d_ci, d_v, d_o, g.n, g.nnz, d_H, g.n, K, d_t,
+                                           len(p.tasks), C, trials=2, locality=True)
         assert (m, sl) == (0, 0) or (m in (2, 4, 8, 16, 32, 64) and sl in (1, 2, 4))
+        assert loc in ((0, 0), (2, 1), (2, 2))
         ref32, ref64 = oracle_pair(p, g, H)
         check(C.cpu().numpy(), ref32)
         C.fill_(float("nan"))
@@ -557,3 +558,26 @@ def test_tune_schedule(gpu_ctx):
         assert e.value.status == capi.INVALID_ARG
     finally:
         gpu_ctx.set_schedule(0, 0)
+        gpu_ctx.set_locality(0, 0)
+
+
+def test_run_order_reused_across_task_lists(gpu_ctx):
+    """With runs sorted by output row, the order is kept between calls and
+    rebuilt when the task array changes; each list's result is right."""
+    g = workloads.small(5, seed=4)
+    K = 32
+    H = synth.features(g.n, K, 6)
+    torch = torch_mod()
+    gpu_ctx.set_schedule(2, 1)
+    gpu_ctx.set_locality(2, 2)
+    try:
+        for S in (3, 7, 3):
+            p = problem(g, SKEWED_COSTS, S)
+            for _ in range(2):
+                got, _ = run_gpu(gpu_ctx, p, H)
+                ref32, ref64 = oracle_pair(p, g, H)
+                check(got, ref32)
+                check(got, ref64)
+    finally:
+        gpu_ctx.set_schedule(0, 0)
+        gpu_ctx.set_locality(0, 0)
