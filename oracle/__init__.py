@@ -1,4 +1,4 @@
-"""ctypes binding of the oracle (test infrastructure: the checker only).
+"""ctypes binding of the oracle (test infrastructure only).
 
 Only tests/, ``__graft_entry__.smoke()`` and bench.py's ``cpu_baseline`` leg
 import this package.  The product library (``cwlb-spmm_amd``) never does.

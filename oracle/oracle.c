@@ -1,8 +1,8 @@
 /*
  * oracle.c -- CPU restatement of CWLB-SpMM's FP32 mean-aggregation path.
  *
- * TEST INFRASTRUCTURE ONLY.  This file is the checker: tests/, the smoke
- * check of __graft_entry__ and the cpu_baseline leg of bench.py load it.  The
+ * TEST INFRASTRUCTURE ONLY: tests/, the smoke check of __graft_entry__ and
+ * the cpu_baseline leg of bench.py load it.  The
  * product path (libcwlb.so) never links, loads or calls it.
  *
  * Each function names the reference file:line it restates.  How each one is

@@ -1,7 +1,7 @@
 #!/usr/bin/env bash
 # Builds oracle/_ref/libcwlb_ref.so: the reference's own pure-C++17 host
 # functions for this path, compiled from the sources where they lie under
-# /root/reference.  Test infrastructure only (the checker of the oracle).
+# /root/reference.  Test infrastructure only: its results pin the oracle.
 #
 # What is compiled, by line range (nothing else of the reference builds here:
 # its kernels need a SYCL compiler, its reorder needs oneDPL/TBB and its

@@ -183,3 +183,44 @@ def test_context_without_gpu_fails_cleanly():
     with pytest.raises(capi.CwlbError) as e:
         capi.Context(0)
     assert e.value.status in (capi.HIP_ERROR, capi.INVALID_ARG)
+
+
+def cxx_header_functions():
+    """Free functions and members declared in the C++17 drop-in headers."""
+    names = set()
+    for h in ("Matrix.h", "utils.h", "parallelMatrix.h", "data.h", "cwlb_device.h",
+              "cwlb_driver.h"):
+        text = open(os.path.join(paths.INCLUDE_DIR, h)).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        text = re.sub(r"//[^\n]*", "", text)
+        for m in re.finditer(r"(?m)^\s*(?:[\w:<>,*&]+\s+)+?[*&]?(\w+)\s*\(", text):
+            name = m.group(1)
+            # declarations only: a body in the header is inline, not exported
+            depth, i = 1, m.end()
+            while depth and i < len(text):
+                depth += {"(": 1, ")": -1}.get(text[i], 0)
+                i += 1
+            after = text[i:].lstrip()
+            if after.startswith("const"):
+                after = after[5:].lstrip()
+            if not after.startswith(";"):
+                continue
+            if name not in ("if", "return", "check", "operator", "explicit", "inline"):
+                names.add(name)
+    return sorted(names)
+
+
+def test_library_exports_the_cxx_layer():
+    """Every function the drop-in headers declare is defined in libcwlb.so."""
+    import subprocess
+    out = subprocess.run(["nm", "-DC", "--defined-only", capi.lib_path()], capture_output=True,
+                         text=True, check=True).stdout
+    declared = cxx_header_functions()
+    for must in ("spmmKernel", "spmmKernelLargeKFallback", "costWeightedTaskPartitioning",
+                 "costWeightedTaskPartitioning_HIP", "loadDatasetToCSR", "sortCSRByDegreeDPLCPU",
+                 "sortCSRByDegree_HIP", "measure_spmm_costs", "run_single_s",
+                 "validate_custom_csr_result", "wave_based_s", "capacity_from_s"):
+        assert must in declared, must
+    missing = [f for f in declared if not re.search(r"(?:^|[ :])" + f + r"\(", out, re.M)]
+    assert not missing, missing
+    assert re.search(r" CSR::CSR\(", out) and re.search(r" cwlb::Device::Device\(", out)

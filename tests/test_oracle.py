@@ -1,4 +1,4 @@
-"""Pins the oracle (oracle/oracle.c) before it is trusted as the checker.
+"""Pins the oracle (oracle/oracle.c) before the other tests rely on it.
 
 Checks, per function:
   partition   the reference's own costWeightedTaskPartitioning compiled from
