@@ -28,9 +28,12 @@
 //     per-work-item loop);
 //   * a long chunk runs on all slots at once, UL nonzeros in flight per
 //     slot, followed by a shuffle reduction across slots;
-//   * column indices and values are fetched 64 at a time with one coalesced
-//     streaming load and handed to the slots with cross-lane shuffles; C is
-//     written with streaming stores.
+//   * column indices and values are fetched with coalesced streaming loads:
+//     64 at a time for a long chunk, handed to the slots with cross-lane
+//     shuffles; for a group of short rows, the group's whole contiguous
+//     range (up to 256 nonzeros) at once, into a per-wave LDS window, so no
+//     row waits on an index load before its feature-row loads.  C is written
+//     with streaming stores.
 // Split rows are cleared by zero_first_segments before the main kernel, by
 // the run that owns their first segment, so each is cleared exactly once.
 #include "internal.h"
@@ -196,6 +199,16 @@ __device__ __forceinline__ Chunk row_chunk(const int* __restrict__ rp, int r, in
 
 constexpr int cmin(int a, int b) { return a < b ? a : b; }
 
+// x, opaque to the optimiser.  Lane-derived values (lane ids, shuffle
+// sources) computed from it inside a loop stay there: hoisted to the kernel
+// entry they would each hold a VGPR for the whole kernel, which costs the
+// aggregation kernel a wave per SIMD (4 instead of 5 at K = 32 and 64).
+__device__ __forceinline__ int fresh(int x)
+{
+    asm volatile("" : "+v"(x));
+    return x;
+}
+
 // Bounds of run `run` (tasks [run*M, min(run*M + M, n_tasks))) as one task.
 struct RunTask {
     int rs, re, fo, ln;
@@ -255,6 +268,15 @@ spmm_mean_runs(const int* __restrict__ rp, const int* __restrict__ ci,
     constexpr int UL = cmin(U, G);                 // nonzeros per slot per step (long rows)
     constexpr int STEP = NS * UL;                  // nonzeros per wave step (<= 64)
     constexpr int kLong = GROUP > 2 ? GROUP : 2;   // chunk length that runs on all slots
+    // A short-row group holds at most GROUP * (kLong - 1) nonzeros.  Beyond
+    // one 64-entry register window, up to kStage of them are staged in a
+    // per-wave LDS window, so no row waits on a column-index load before
+    // its feature-row loads.
+    constexpr int kMaxGroupNnz = GROUP * (kLong - 1);
+    constexpr int kStage = kMaxGroupNnz > 64 ? cmin(kMaxGroupNnz, 256) : 0;
+    constexpr int kWin = kStage > 0 ? kStage : 64;  // nonzeros of one group
+    __shared__ int s_col[kWaves * (kStage > 0 ? kStage : 1)];
+    __shared__ float s_val[kWaves * (kStage > 0 ? kStage : 1)];
 
     const int lane = threadIdx.x & 63;
     const int slot = lane / G;
@@ -263,8 +285,11 @@ spmm_mean_runs(const int* __restrict__ rp, const int* __restrict__ ci,
     long long jb;
     block_slice<SL>(slice, jb, chunk);
     if (jb >= n_blocks) return;
-    const long long pos = jb * kWaves + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const long long pos = jb * kWaves + wv;
     if (pos >= n_runs) return;
+    int* __restrict__ wcol = s_col + wv * (kStage > 0 ? kStage : 1);
+    float* __restrict__ wval = s_val + wv * (kStage > 0 ? kStage : 1);
     // run_order (optional) is a permutation of [0, n_runs): runs execute in
     // that order instead of task order.
     const long long run = run_order ? static_cast<long long>(run_order[pos]) : pos;
@@ -296,6 +321,7 @@ spmm_mean_runs(const int* __restrict__ rp, const int* __restrict__ ci,
                 for (int q = 0; q < R; ++q) acc[q] = vzero<VEC>();
                 for (int w0 = c0.b; w0 < c0.e; w0 += 64) {
                     const int wn = min(64, c0.e - w0);
+                    const int lane = fresh(threadIdx.x & 63);
                     int colw = 0;
                     float valw = 0.0f;
                     if (lane < wn) {
@@ -306,9 +332,10 @@ spmm_mean_runs(const int* __restrict__ rp, const int* __restrict__ ci,
                         int cc[UL];
                         float a[UL];
                         bool ok[UL];
+                        const int sl = fresh(slot);
 #pragma unroll
                         for (int u = 0; u < UL; ++u) {
-                            const int jj = k0 + u * NS + slot;
+                            const int jj = k0 + u * NS + sl;
                             cc[u] = __shfl(colw, jj & 63);
                             a[u] = __shfl(valw, jj & 63);
                             ok[u] = jj < wn;
@@ -367,22 +394,61 @@ spmm_mean_runs(const int* __restrict__ rp, const int* __restrict__ ci,
             }
 
             // ---------------- short rows: one row per slot, RU rows per slot
+            const int lane = fresh(threadIdx.x & 63);
             const int rr = r + lane;
             const bool mine = lane < GROUP && rr < rhi;
             Chunk my = {0, 0, 0, 0};
             if (mine) my = row_chunk(rp, rr, rs, re, fo, ln, nnz);
             const int mylen = my.e - my.b;
-            const unsigned long long lm = __ballot(mine && mylen >= kLong);
-            int cnt = min(GROUP, rhi - r);
-            if (lm) cnt = min(cnt, static_cast<int>(__ffsll(static_cast<long long>(lm))) - 1);
-            const int myo = (mine && lane < cnt) ? origin[rr] : 0;
-            // Nonzeros of the group are contiguous: [gs, ge).
+            // The group: the leading rows that are short, start where the
+            // previous row's chunk ends (always, for a non-decreasing
+            // row_ptr) and end within kWin nonzeros of the group's start.
+            // The first row always qualifies (its chunk is shorter than
+            // kLong <= kWin), so every group makes progress, and the
+            // group's nonzeros are the contiguous range [gs, gs + gn).
+            const int mys = my.base + my.b;
+            const int mye = my.base + my.e;
             const int gs = c0.base + c0.b;
-            const int ge = __shfl(my.base + my.e, cnt - 1);
-            const bool win = (ge - gs) <= 64 && ge >= gs;
+            const int prev_end = __shfl_up(mye, 1);
+            const bool fits = mine && mylen < kLong && (lane == 0 || mys == prev_end) &&
+                              mye - gs <= kWin;
+            const unsigned long long stop = __ballot(!fits);
+            int cnt = min(GROUP, rhi - r);
+            if (stop) cnt = min(cnt, static_cast<int>(__ffsll(static_cast<long long>(stop))) - 1);
+            const int myo = (mine && lane < cnt) ? origin[rr] : 0;
+            const int ge = __shfl(mye, cnt - 1);
+            const int gn = (gs >= 0 && static_cast<long long>(ge) <= nnz) ? ge - gs : 0;
             int colw = 0;
             float valw = 0.0f;
-            if (win && lane < ge - gs && gs >= 0 && static_cast<long long>(gs) + lane < nnz) {
+            if constexpr (kStage > 0) {
+                // The previous group's reads of this wave's window are done
+                // (wave-ordered LDS); the fences keep the compiler from
+                // moving accesses across the exchange.
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                // All loads first, then the LDS writes: one memory round trip.
+                constexpr int NT = (kStage + 63) / 64;
+                int lc[NT];
+                float lv[NT];
+#pragma unroll
+                for (int t = 0; t < NT; ++t) {
+                    const int i = lane + 64 * t;
+                    lc[t] = i < gn ? __builtin_nontemporal_load(ci + gs + i) : 0;
+                    lv[t] = i < gn ? __builtin_nontemporal_load(val + gs + i) : 0.0f;
+                }
+#pragma unroll
+                for (int t = 0; t < NT; ++t) {
+                    const int i = lane + 64 * t;
+                    if (i < gn) {
+                        wcol[i] = lc[t];
+                        wval[i] = lv[t];
+                    }
+                }
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            } else if (lane < gn) {
                 colw = __builtin_nontemporal_load(ci + gs + lane);
                 valw = __builtin_nontemporal_load(val + gs + lane);
             }
@@ -392,8 +458,8 @@ spmm_mean_runs(const int* __restrict__ rp, const int* __restrict__ ci,
             int maxlen = 0;
 #pragma unroll
             for (int u = 0; u < RU; ++u) {
-                const int gi = u * NS + slot;
-                pos[u] = __shfl(my.base + my.b, gi);
+                const int gi = u * NS + fresh(slot);
+                pos[u] = __shfl(mys - gs, gi);  // window position of the chunk
                 len[u] = __shfl(mylen, gi);
                 if (gi >= cnt) len[u] = 0;
                 maxlen = max(maxlen, len[u]);
@@ -407,15 +473,14 @@ spmm_mean_runs(const int* __restrict__ rp, const int* __restrict__ ci,
                 bool ok[RU];
 #pragma unroll
                 for (int u = 0; u < RU; ++u) {
-                    const int gp = pos[u] + j;
                     ok[u] = j < len[u];
-                    if (win) {
-                        const int src = (gp - gs) & 63;
-                        cc[u] = __shfl(colw, src);
-                        a[u] = __shfl(valw, src);
+                    const int src = pos[u] + j;  // in [0, gn) whenever ok[u]
+                    if constexpr (kStage > 0) {
+                        cc[u] = wcol[ok[u] ? src : 0];
+                        a[u] = wval[ok[u] ? src : 0];
                     } else {
-                        cc[u] = ok[u] ? ci[gp] : 0;
-                        a[u] = ok[u] ? val[gp] : 0.0f;
+                        cc[u] = __shfl(colw, src & 63);
+                        a[u] = __shfl(valw, src & 63);
                     }
                     if (ok[u] && static_cast<unsigned long long>(cc[u]) >=
                                      static_cast<unsigned long long>(h_rows)) {
@@ -443,7 +508,7 @@ spmm_mean_runs(const int* __restrict__ rp, const int* __restrict__ ci,
             }
 #pragma unroll
             for (int u = 0; u < RU; ++u) {
-                const int gi = u * NS + slot;
+                const int gi = u * NS + fresh(slot);
                 const int o = __shfl(myo, gi);
                 const int d = __shfl(my.d, gi);
                 const int b = __shfl(my.b, gi);

@@ -337,6 +337,30 @@ def test_duplicate_columns_and_values(gpu_ctx, sched, rng):
         check(got, ref64)
 
 
+@pytest.mark.parametrize("K", [16, 32, 64])
+@pytest.mark.parametrize("d", [1, 2, 3, 5, 8, 9, 16, 31])
+def test_short_row_windows_bit_exact(gpu_ctx, sched, K, d, rng):
+    """Groups of short rows whose nonzeros fit the 64-entry register window,
+    the per-wave LDS window (up to 256) or neither (per-lane loads).  Every
+    row is whole; rows shorter than 16 nonzeros run row-per-slot under every
+    schedule, are summed in CSR order and match the oracle bit for bit
+    (longer rows may take the all-slots path, whose shuffle reduction
+    regroups the sum)."""
+    n = 3000
+    deg = rng.integers(max(d - 2, 0), d + 1, n)
+    rp = np.concatenate([[0], np.cumsum(deg)]).astype(np.int32)
+    ci = rng.integers(0, n, rp[-1]).astype(np.int32)
+    val = rng.uniform(-2, 2, rp[-1]).astype(np.float32)
+    g = custom_graph(rp, ci, val)
+    H = synth.features(n, K, d)
+    p = problem(g, UNIT_COSTS, 100000)
+    got, _ = run_gpu(gpu_ctx, p, H, flags=sched)
+    ref32 = oracle.spmm_mean_f32(p.row_ptr, p.col_idx, p.val, p.origin, H, p.tasks)
+    short = deg < 16
+    assert np.array_equal(got[short], ref32[short])
+    check(got, ref32)
+
+
 def test_unsorted_graph_custom_tasks(gpu_ctx, rng):
     """Caller-made task lists: one task per row, and whole-graph tasks."""
     g = workloads.small(2, seed=5)
