@@ -42,14 +42,17 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def measured_traffic(cfg):
-    """HBM bytes per aggregation launch from the committed rocprofv3 PMC summary."""
+def measured_traffic(cfg, S):
+    """HBM bytes per aggregation launch from the committed rocprofv3 PMC
+    summary: the figure measured at segment size S when the summary has one
+    ("traffic_bytes_per_launch[S=63]: ..."), else its unqualified figure."""
     try:
         text = open(PMC_SUMMARY[cfg]).read()
     except (KeyError, OSError):
         return None
-    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", text)
-    return float(m.group(1)) if m else None
+    found = dict(re.findall(r"traffic_bytes_per_launch(?:\[S=(\d+)\])?:\s*([0-9.eE+]+)", text))
+    value = found.get(str(S), found.get(""))
+    return float(value) if value is not None else None
 
 
 def preprocessing_times(ctx, g, rp, costs, S, tasks, reorder_host_ms):
@@ -240,7 +243,7 @@ def main():
     gflops = flops / (ms_per_step * 1e-3) / 1e9
     b_alg = workloads.algorithmic_bytes(g.n, g.nnz, K, T)
     achieved = b_alg / (main_us * 1e-6) / 1e9
-    traffic = measured_traffic(cfg)
+    traffic = measured_traffic(cfg, S)
 
     cpu = None
     if not args.no_cpu:

@@ -84,6 +84,22 @@ part_transitions(PartParams p, long long V, int* __restrict__ next, int* __restr
     if (overrun) atomicOr(status, 1);
 }
 
+// levels[0] = 1 + the first k with J_k(A(0)) == n (J_k = 2^k steps; the
+// J arrays are consecutive, V entries each), or 0 if none of the L reaches
+// the end.
+__global__ void part_levels(const int* __restrict__ J, long long V, int L, int n,
+                            int* __restrict__ levels)
+{
+    int found = 0;
+    for (int k = 0; k < L; ++k) {
+        if (J[static_cast<long long>(k) * V] == n) {
+            found = k + 1;
+            break;
+        }
+    }
+    *levels = found;
+}
+
 __global__ void __launch_bounds__(kBlock)
 part_double(long long V, const int* __restrict__ src, int* __restrict__ dst)
 {
@@ -224,33 +240,34 @@ cwlb_status launch_partition(cwlb_ctx* ctx, const int32_t* rp, int32_t n,
     // 1. transitions of every node.
     const long long V = static_cast<long long>(n) + 1 + n_long;
     if (V > INT_MAX) return fail(CWLB_UNSUPPORTED, "cwlb_partition_device: too many rows");
-    Mem cnt;
+    // The chain from A(0) has at most V fresh nodes, so L doubling levels
+    // (2^(L-1) >= V) always reach the end; all are computed back to back
+    // in one allocation, then one read-back finds how many were needed.
+    int L = 1;
+    while ((1LL << (L - 1)) < V) ++L;
+    Mem cnt, Jall;
     CWLB_HIP_TRY(cnt.alloc(sizeof(int) * V));
-    std::vector<Mem> J(1);
-    CWLB_HIP_TRY(J[0].alloc(sizeof(int) * V));
+    CWLB_HIP_TRY(Jall.alloc(sizeof(int) * static_cast<size_t>(V) * L + sizeof(int)));
+    int* const J0 = Jall.as<int>();
+    auto J = [&](int k) { return J0 + static_cast<long long>(k) * V; };
+    int* const d_levels = J0 + static_cast<long long>(L) * V;
     hipLaunchKernelGGL(part_transitions, dim3(grid_for(V)), dim3(kBlock), 0, st, p, V,
-                       J[0].as<int>(), cnt.as<int>(), status.as<int>());
+                       J(0), cnt.as<int>(), status.as<int>());
     CWLB_LAUNCH_CHECK("part_transitions");
-    int bad = 0;
-    CWLB_HIP_TRY(hipMemcpyAsync(&bad, status.p, sizeof(int), hipMemcpyDeviceToHost, st));
-    CWLB_HIP_TRY(hipStreamSynchronize(st));
-    if (bad) return fail(CWLB_RUNTIME_ERROR, "cwlb_partition_device: a row scan exceeded its bound");
-
-    // 2. doubling until 2^k steps from A(0) reach the end.
-    int levels = 1;
-    for (;;) {
-        int at = 0;
-        CWLB_HIP_TRY(hipMemcpyAsync(&at, J[levels - 1].as<int>(), sizeof(int), hipMemcpyDeviceToHost, st));
-        CWLB_HIP_TRY(hipStreamSynchronize(st));
-        if (at == n) break;
-        if (levels >= 40) return fail(CWLB_RUNTIME_ERROR, "cwlb_partition_device: chain too long");
-        J.emplace_back();
-        CWLB_HIP_TRY(J.back().alloc(sizeof(int) * V));
-        hipLaunchKernelGGL(part_double, dim3(grid_for(V)), dim3(kBlock), 0, st, V,
-                           J[levels - 1].as<int>(), J[levels].as<int>());
+    // 2. doubling: J_{k+1} = J_k o J_k.
+    for (int k = 1; k < L; ++k) {
+        hipLaunchKernelGGL(part_double, dim3(grid_for(V)), dim3(kBlock), 0, st, V, J(k - 1), J(k));
         CWLB_LAUNCH_CHECK("part_double");
-        ++levels;
     }
+    hipLaunchKernelGGL(part_levels, dim3(1), dim3(1), 0, st, J0, V, L, n, d_levels);
+    CWLB_LAUNCH_CHECK("part_levels");
+    int host_status[2] = {0, 0};
+    CWLB_HIP_TRY(hipMemcpyAsync(&host_status[0], status.p, sizeof(int), hipMemcpyDeviceToHost, st));
+    CWLB_HIP_TRY(hipMemcpyAsync(&host_status[1], d_levels, sizeof(int), hipMemcpyDeviceToHost, st));
+    CWLB_HIP_TRY(hipStreamSynchronize(st));
+    if (host_status[0]) return fail(CWLB_RUNTIME_ERROR, "cwlb_partition_device: a row scan exceeded its bound");
+    const int levels = host_status[1];
+    if (levels <= 0) return fail(CWLB_RUNTIME_ERROR, "cwlb_partition_device: chain too long");
     // J[levels-1] maps A(0) to the end: the chain has at most 2^(levels-1)
     // fresh nodes before the end.
     const long long len = 1LL << (levels - 1);
@@ -263,7 +280,7 @@ cwlb_status launch_partition(cwlb_ctx* ctx, const int32_t* rp, int32_t n,
         const long long half = 1LL << j;
         const long long count = len / (2 * half);
         hipLaunchKernelGGL(part_expand, dim3(grid_for(count)), dim3(kBlock), 0, st, count, half,
-                           J[j].as<int>(), chain.as<int>());
+                           J(j), chain.as<int>());
         CWLB_LAUNCH_CHECK("part_expand");
     }
     // 4. task offsets of the chain nodes.

@@ -9,8 +9,10 @@
 //      degree needs (rocPRIM): equal degrees keep ascending original ids, so
 //      the order is the reference comparator's (degree, id) order;
 //   3. row_ptr_out = 0 followed by the inclusive scan of the sorted degrees;
-//   4. gather_rows: each reordered row copies its entries from the original
-//      row, a lane per short row, the whole wave on rows longer than 16.
+//   4. gather_rows / gather_long: each reordered row copies its entries from
+//      the original row: a lane per row of at most 16 entries; the longer
+//      rows (a suffix of the sorted order) as one contiguous output range
+//      cut into equal chunks, so no wave copies a hub row alone.
 // The call synchronises on the context's stream.
 #include <rocprim/device/device_radix_sort.hpp>
 #include <rocprim/device/device_scan.hpp>
@@ -23,6 +25,7 @@ namespace {
 
 constexpr int kBlock = 256;
 constexpr int kLaneRowMax = 16;
+constexpr int kLongChunk = kBlock * 16;  // entries per gather_long block
 
 // status bit 0: an offset outside [0, nnz] or a decreasing pair.  Each
 // block writes its maximum degree to block_max[blockIdx.x] (one contended
@@ -76,37 +79,82 @@ reduce_max(const unsigned* __restrict__ v, long long n, unsigned* __restrict__ o
     }
 }
 
+// Rows of at most kLaneRowMax entries: a lane per row.  Longer rows are
+// gathered by gather_long.
 __global__ void __launch_bounds__(kBlock)
 gather_rows(const int* __restrict__ rp, const int* __restrict__ ci, const float* __restrict__ val,
             const int* __restrict__ origin, const int* __restrict__ rp_out, int n,
             int* __restrict__ ci_out, float* __restrict__ val_out)
 {
-    const int lane = threadIdx.x & 63;
     const int r = blockIdx.x * kBlock + threadIdx.x;
-    int src = 0, dst = 0, len = 0;
-    if (r < n) {
-        const int o = origin[r];
-        src = rp[o];
-        dst = rp_out[r];
-        len = rp_out[r + 1] - dst;
+    if (r >= n) return;
+    const int dst = rp_out[r];
+    const int len = rp_out[r + 1] - dst;
+    if (len > kLaneRowMax) return;
+    const int src = rp[origin[r]];
+    for (int j = 0; j < len; ++j) {
+        ci_out[dst + j] = ci[src + j];
+        val_out[dst + j] = val[src + j];
     }
-    if (len <= kLaneRowMax) {
-        for (int j = 0; j < len; ++j) {
-            ci_out[dst + j] = ci[src + j];
-            val_out[dst + j] = val[src + j];
-        }
+}
+
+// long_row[0] = the first reordered row with more than kLaneRowMax entries
+// (n if none): the degrees are sorted ascending, so those rows are a suffix.
+__global__ void find_long_rows(const unsigned* __restrict__ sorted_deg, int n,
+                               int* __restrict__ long_row)
+{
+    int lo = 0, hi = n;
+    while (lo < hi) {
+        const int mid = lo + (hi - lo) / 2;
+        if (sorted_deg[mid] > static_cast<unsigned>(kLaneRowMax)) hi = mid;
+        else lo = mid + 1;
     }
-    unsigned long long m = __ballot(len > kLaneRowMax);
-    while (m) {
-        const int l = __ffsll(static_cast<long long>(m)) - 1;
-        m &= m - 1;
-        const int s = __shfl(src, l);
-        const int d = __shfl(dst, l);
-        const int c = __shfl(len, l);
-        for (int j = lane; j < c; j += 64) {
-            ci_out[d + j] = ci[s + j];
-            val_out[d + j] = val[s + j];
+    *long_row = lo;
+}
+
+// The entries of the long rows [long_row, n), which fill the output range
+// [rp_out[long_row], nnz): block b copies the kLongChunk entries from
+// rp_out[long_row] + b * kLongChunk on, a thread every kBlock-th entry, so a
+// hub row is spread over many blocks and every access is coalesced.  The
+// first row of the block's range is found by binary search; each thread then
+// walks forward row by row.
+__global__ void __launch_bounds__(kBlock)
+gather_long(const int* __restrict__ rp, const int* __restrict__ ci, const float* __restrict__ val,
+            const int* __restrict__ origin, const int* __restrict__ rp_out, int n,
+            const int* __restrict__ long_row, int* __restrict__ ci_out, float* __restrict__ val_out)
+{
+    __shared__ int first_row;
+    const int r0 = *long_row;
+    if (r0 >= n) return;
+    const long long begin = static_cast<long long>(rp_out[r0]) +
+                            static_cast<long long>(blockIdx.x) * kLongChunk;
+    const long long end = rp_out[n];
+    if (begin >= end) return;
+    if (threadIdx.x == 0) {
+        int lo = r0, hi = n - 1;  // last row whose start is <= begin
+        while (lo < hi) {
+            const int mid = hi - (hi - lo) / 2;
+            if (rp_out[mid] <= begin) lo = mid;
+            else hi = mid - 1;
         }
+        first_row = lo;
+    }
+    __syncthreads();
+    int row = first_row;
+    int row_begin = rp_out[row];
+    int row_end = rp_out[row + 1];
+    int src = rp[origin[row]];
+    const long long stop = min(end, begin + kLongChunk);
+    for (long long p = begin + threadIdx.x; p < stop; p += kBlock) {
+        while (p >= row_end) {
+            ++row;
+            row_begin = row_end;
+            row_end = rp_out[row + 1];
+            src = rp[origin[row]];
+        }
+        const long long s = src + (p - row_begin);
+        ci_out[p] = ci[s];
+        val_out[p] = val[s];
     }
 }
 
@@ -276,7 +324,16 @@ cwlb_status launch_reorder(cwlb_ctx* ctx, int32_t n, int64_t nnz, const int32_t*
     if (nnz > 0) {
         hipLaunchKernelGGL(gather_rows, dim3(grid), dim3(kBlock), 0, st, rp, ci, val, origin,
                            rp_out, n, ci_out, val_out);
-        CWLB_HIP_TRY(hipGetLastError());
+        CWLB_LAUNCH_CHECK("gather_rows");
+        // d_status[0] is free again (checked above): it receives the first
+        // long row.  The long rows hold at most nnz entries.
+        hipLaunchKernelGGL(find_long_rows, dim3(1), dim3(1), 0, st, d_sorted, n, d_status);
+        CWLB_LAUNCH_CHECK("find_long_rows");
+        const unsigned long_grid =
+            static_cast<unsigned>((static_cast<uint64_t>(nnz) + kLongChunk - 1) / kLongChunk);
+        hipLaunchKernelGGL(gather_long, dim3(long_grid), dim3(kBlock), 0, st, rp, ci, val,
+                           origin, rp_out, n, d_status, ci_out, val_out);
+        CWLB_LAUNCH_CHECK("gather_long");
     }
     CWLB_HIP_TRY(hipStreamSynchronize(st));
     return CWLB_OK;

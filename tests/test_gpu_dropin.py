@@ -75,7 +75,11 @@ def test_device_reorder_edge_cases(gpu_ctx, rng):
                             np.zeros(0, np.float32))
     assert list(got[1]) == [0]
     # all rows empty, then hub rows next to empty and short rows, values kept
-    for degs in (np.zeros(1000, np.int64), np.array([0, 3000, 1, 17, 16, 0, 64, 65, 3000, 2])):
+    # the long rows (more than 16 entries) are copied in chunks of 4,096
+    # output entries: rows ending on, just before and just after a chunk end
+    chunked = np.array([17] * 300 + [4095, 4096, 4097, 12289, 16, 0, 1] + [40] * 77, np.int64)
+    for degs in (np.zeros(1000, np.int64), np.array([0, 3000, 1, 17, 16, 0, 64, 65, 3000, 2]),
+                 chunked, np.array([9000], np.int64), np.array([17], np.int64)):
         rp = np.concatenate([[0], np.cumsum(degs)]).astype(np.int32)
         ci = rng.integers(0, 50, rp[-1]).astype(np.int32)
         val = rng.normal(size=rp[-1]).astype(np.float32)
