@@ -35,6 +35,7 @@ PMC_SUMMARY = {
     4: os.path.join(ROOT, "profiles", "spmm_mean_runs_rmat22_k128_pmc.txt"),
     5: os.path.join(ROOT, "profiles", "spmm_mean_runs_mesh16m_k32_trace_pmc.md"),
     3: os.path.join(ROOT, "profiles", "spmm_mean_runs_sbm240k_k600_trace_pmc.md"),
+    2: os.path.join(ROOT, "profiles", "spmm_mean_runs_chunglu1m_k64_trace_pmc.md"),
 }
 
 
