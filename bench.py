@@ -106,6 +106,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--cfg", type=int, default=4, help="workload configuration (default: R-MAT)")
     ap.add_argument("--s", type=int, default=0, help="fixed segment size (0 = best candidate)")
+    ap.add_argument("--k", type=int, default=0,
+                    help="feature width instead of the workload's (above the device's maximum "
+                         "work-group size the large-K entry runs, as the reference's driver "
+                         "picks spmmKernelLargeKFallback)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--tasks-per-wave", type=int, default=0,
@@ -137,7 +141,8 @@ def main():
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     cfg = args.cfg
-    K = workloads.FEATURE_DIM[cfg]
+    K = args.k or workloads.FEATURE_DIM[cfg]
+    workload = workloads.NAMES[cfg] if not args.k else f"{workloads.NAMES[cfg].rsplit('_k', 1)[0]}_k{K}"
     t0 = time.time()
     g = workloads.graph(cfg)
     log(f"graph {workloads.NAMES[cfg]}: n={g.n} nnz={g.nnz} ({time.time() - t0:.1f}s)")
@@ -150,6 +155,7 @@ def main():
     stream = torch.cuda.current_stream()
     ctx = capi.Context(0, stream.cuda_stream)
     info = ctx.info()
+    large_k = K > info.max_work_group_size
     dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()  # noqa: E731
     d_rp, d_ci, d_v, d_o = dev(rp), dev(ci), dev(val), dev(origin)
     H = torch.empty((g.n, K), dtype=torch.float32, device="cuda")
@@ -161,7 +167,8 @@ def main():
         return capi.partition(rp, costs, cap)
 
     def call(d_t, n_t, timed):
-        return ctx.spmm(d_rp, d_ci, d_v, d_o, g.n, g.nnz, H, g.n, K, d_t, n_t, C, timed=timed)
+        return ctx.spmm(d_rp, d_ci, d_v, d_o, g.n, g.nnz, H, g.n, K, d_t, n_t, C, timed=timed,
+                        large_k=large_k)
 
     # S: the best of the three wave-based candidates (main.cpp:534-577), or fixed.
     cands = [args.s] if args.s else workloads.candidate_s(g.nnz, info.compute_units)
@@ -215,7 +222,7 @@ def main():
     # The reference's structure (one task per wave, one atomic add per
     # partial segment), for comparison.
     pt = [ctx.spmm(d_rp, d_ci, d_v, d_o, g.n, g.nnz, H, g.n, K, d_t, T, C,
-                   flags=capi.PER_TASK) for _ in range(10)]
+                   flags=capi.PER_TASK, large_k=large_k) for _ in range(10)]
     per_task_us = float(np.mean([t.total_us for t in pt]))
     log(f"S={S} T={T} ms/step={ms_per_step:.3f} main_us={main_us:.1f} zero_us={zero_us:.1f}")
 
@@ -244,7 +251,7 @@ def main():
     gflops = flops / (ms_per_step * 1e-3) / 1e9
     b_alg = workloads.algorithmic_bytes(g.n, g.nnz, K, T)
     achieved = b_alg / (main_us * 1e-6) / 1e9
-    traffic = measured_traffic(cfg, S)
+    traffic = measured_traffic(cfg, S) if not args.k else None
 
     cpu = None
     if not args.no_cpu:
@@ -287,7 +294,7 @@ def main():
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic",
-        "config": {"workload": workloads.NAMES[cfg], "n": g.n, "nnz": g.nnz, "K": K, "S": S,
+        "config": {"workload": workload, "n": g.n, "nnz": g.nnz, "K": K, "S": S,
                    "tasks": T, "costs": list(costs), "device": info.name.decode(),
                    "main_kernel_us": round(main_us, 2), "zero_pass_us": round(zero_us, 2),
                    "per_task_mode_us": round(per_task_us, 2),
