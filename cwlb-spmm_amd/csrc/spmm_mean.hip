@@ -268,10 +268,11 @@ spmm_mean_runs(const int* __restrict__ rp, const int* __restrict__ ci,
     constexpr int UL = cmin(U, G);                 // nonzeros per slot per step (long rows)
     constexpr int STEP = NS * UL;                  // nonzeros per wave step (<= 64)
     constexpr int kLong = GROUP > 2 ? GROUP : 2;   // chunk length that runs on all slots
-    // A short-row group holds at most GROUP * (kLong - 1) nonzeros.  Beyond
-    // one 64-entry register window, up to kStage of them are staged in a
-    // per-wave LDS window, so no row waits on a column-index load before
-    // its feature-row loads.
+    // A short-row group holds at most GROUP * (kLong - 1) nonzeros.  When
+    // that can exceed 64, a group's nonzeros (up to kStage, the group is cut
+    // there) go through a per-wave LDS window; otherwise through one
+    // 64-entry register window.  Either way no row waits on a column-index
+    // load before its feature-row loads.
     constexpr int kMaxGroupNnz = GROUP * (kLong - 1);
     constexpr int kStage = kMaxGroupNnz > 64 ? cmin(kMaxGroupNnz, 256) : 0;
     constexpr int kWin = kStage > 0 ? kStage : 64;  // nonzeros of one group
