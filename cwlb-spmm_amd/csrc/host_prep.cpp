@@ -12,6 +12,8 @@
 #include <fstream>
 #include <iomanip>
 #include <string>
+#include <thread>
+#include <utility>
 #include <vector>
 
 #include "cwlb.h"
@@ -21,6 +23,29 @@ cwlb_status fail(cwlb_status st, const std::string& msg);
 }
 
 namespace {
+
+// ---------------------------------------------------------------------------
+// Threads for the host reordering: up to 16 (the host share of one GPU),
+// about one per 256K rows + nonzeros, at least one.
+constexpr int32_t kDenseDegrees = 1 << 16;
+
+int reorder_threads(int32_t n_rows, int64_t nnz)
+{
+    const unsigned hw = std::max(1u, std::thread::hardware_concurrency());
+    const int64_t by_size = (static_cast<int64_t>(n_rows) + nnz) / (1 << 18) + 1;
+    return static_cast<int>(std::min<int64_t>({static_cast<int64_t>(hw), 16, by_size}));
+}
+
+// fn(t) for t in [0, T): on T - 1 new threads and the caller's.
+template <class Fn>
+void parallel_for(int T, Fn fn)
+{
+    std::vector<std::thread> pool;
+    pool.reserve(static_cast<size_t>(T > 0 ? T - 1 : 0));
+    for (int t = 1; t < T; ++t) pool.emplace_back(fn, t);
+    fn(0);
+    for (std::thread& th : pool) th.join();
+}
 
 // ---------------------------------------------------------------------------
 // Cost-weighted partition (reference src/utils.cpp:832-1021).
@@ -183,6 +208,9 @@ cwlb_status cwlb_partition(const int32_t* row_ptr, int32_t n_rows, const cwlb_co
 
 // Degree reordering (reference main.cpp:197-278): a stable counting sort by
 // degree gives the (degree, original id) order of the reference comparator.
+// It runs on up to 16 threads over contiguous row chunks (per-chunk
+// histograms, then positions in chunk order, so equal degrees keep
+// ascending ids), as the reference's oneDPL/TBB sort runs on all cores.
 cwlb_status cwlb_reorder_by_degree(int32_t n_rows, int64_t nnz, const int32_t* row_ptr,
                                    const int32_t* col_idx, const float* val, int32_t* origin,
                                    int32_t* row_ptr_out, int32_t* col_idx_out, float* val_out)
@@ -196,34 +224,107 @@ cwlb_status cwlb_reorder_by_degree(int32_t n_rows, int64_t nnz, const int32_t* r
     if (!row_ptr || !origin || !row_ptr_out || (nnz > 0 && (!col_idx || !val || !col_idx_out ||
                                                             !val_out)))
         return cwlb::fail(CWLB_INVALID_ARG, "cwlb_reorder_by_degree: null pointer");
-    int32_t maxdeg = 0;
-    for (int32_t i = 0; i < n_rows; ++i) {
-        const int32_t d = row_ptr[i + 1] - row_ptr[i];
-        if (d < 0 || row_ptr[i] < 0 || row_ptr[i + 1] > nnz)
-            return cwlb::fail(CWLB_INVALID_ARG, "cwlb_reorder_by_degree: row_ptr not a CSR offset array");
-        maxdeg = std::max(maxdeg, d);
-    }
-    std::vector<int64_t> start(static_cast<size_t>(maxdeg) + 2, 0);
-    for (int32_t i = 0; i < n_rows; ++i) ++start[row_ptr[i + 1] - row_ptr[i] + 1];
-    for (int32_t d = 0; d <= maxdeg; ++d) start[d + 1] += start[d];
-    for (int32_t i = 0; i < n_rows; ++i) origin[start[row_ptr[i + 1] - row_ptr[i]]++] = i;
-    int64_t acc = 0;
-    row_ptr_out[0] = 0;
-    for (int32_t r = 0; r < n_rows; ++r) {
-        acc += row_ptr[origin[r] + 1] - row_ptr[origin[r]];
-        row_ptr_out[r + 1] = static_cast<int32_t>(acc);
-    }
-    if (acc != nnz)
+    const int T = reorder_threads(n_rows, nnz);
+    const auto lo = [&](int t) { return static_cast<int32_t>(static_cast<int64_t>(n_rows) * t / T); };
+
+    // 1. Validation and per-thread histograms of the degrees below
+    //    kDenseDegrees; heavier rows are rare (at most nnz / kDenseDegrees)
+    //    and are ordered separately.
+    std::vector<std::vector<int64_t>> hist(static_cast<size_t>(T));
+    std::vector<std::vector<std::pair<int32_t, int32_t>>> heavy(static_cast<size_t>(T));
+    std::vector<int32_t> maxdeg(static_cast<size_t>(T), 0);
+    std::vector<char> bad(static_cast<size_t>(T), 0);
+    parallel_for(T, [&](int t) {
+        std::vector<int64_t>& h = hist[static_cast<size_t>(t)];
+        int32_t m = 0;
+        for (int32_t i = lo(t); i < lo(t + 1); ++i) {
+            const int32_t d = row_ptr[i + 1] - row_ptr[i];
+            if (d < 0 || row_ptr[i] < 0 || row_ptr[i + 1] > nnz) {
+                bad[static_cast<size_t>(t)] = 1;
+                return;
+            }
+            m = std::max(m, d);
+            if (d < kDenseDegrees) {
+                if (static_cast<size_t>(d) >= h.size()) h.resize(static_cast<size_t>(d) + 1, 0);
+                ++h[static_cast<size_t>(d)];
+            }
+        }
+        maxdeg[static_cast<size_t>(t)] = m;
+    });
+    if (std::any_of(bad.begin(), bad.end(), [](char c) { return c != 0; }))
+        return cwlb::fail(CWLB_INVALID_ARG, "cwlb_reorder_by_degree: row_ptr not a CSR offset array");
+    const int32_t dmax = *std::max_element(maxdeg.begin(), maxdeg.end());
+    const size_t D = static_cast<size_t>(std::min<int32_t>(dmax, kDenseDegrees - 1)) + 1;
+
+    // 2. Stable positions: degree d, thread t starts after every row of a
+    //    smaller degree and every row of degree d in an earlier chunk.
+    std::vector<std::vector<int64_t>> pos(static_cast<size_t>(T), std::vector<int64_t>(D, 0));
+    int64_t running = 0;
+    for (size_t d = 0; d < D; ++d)
+        for (int t = 0; t < T; ++t) {
+            pos[static_cast<size_t>(t)][d] = running;
+            const std::vector<int64_t>& h = hist[static_cast<size_t>(t)];
+            running += d < h.size() ? h[d] : 0;
+        }
+    const int64_t n_light = running;
+
+    // 3. Scatter of the row ids.
+    parallel_for(T, [&](int t) {
+        std::vector<int64_t>& p = pos[static_cast<size_t>(t)];
+        for (int32_t i = lo(t); i < lo(t + 1); ++i) {
+            const int32_t d = row_ptr[i + 1] - row_ptr[i];
+            if (d < kDenseDegrees) origin[p[static_cast<size_t>(d)]++] = i;
+            else heavy[static_cast<size_t>(t)].emplace_back(d, i);
+        }
+    });
+    // Heavy rows in (degree, id) order after all lighter ones; the chunks
+    // are in id order, so a stable sort by degree gives it.
+    std::vector<std::pair<int32_t, int32_t>> all_heavy;
+    for (const auto& v : heavy) all_heavy.insert(all_heavy.end(), v.begin(), v.end());
+    std::stable_sort(all_heavy.begin(), all_heavy.end(),
+                     [](const auto& x, const auto& y) { return x.first < y.first; });
+    for (size_t k = 0; k < all_heavy.size(); ++k)
+        origin[n_light + static_cast<int64_t>(k)] = all_heavy[k].second;
+
+    // 4. Offsets: inclusive scan of the sorted degrees, chunk sums first.
+    std::vector<int64_t> part(static_cast<size_t>(T) + 1, 0);
+    parallel_for(T, [&](int t) {
+        int64_t acc = 0;
+        for (int32_t r = lo(t); r < lo(t + 1); ++r) acc += row_ptr[origin[r] + 1] - row_ptr[origin[r]];
+        part[static_cast<size_t>(t) + 1] = acc;
+    });
+    for (int t = 0; t < T; ++t) part[static_cast<size_t>(t) + 1] += part[static_cast<size_t>(t)];
+    if (part[static_cast<size_t>(T)] != nnz)
         return cwlb::fail(CWLB_RUNTIME_ERROR,
                           "DPL CPU degree reordering produced an inconsistent NNZ count.");
-    for (int32_t r = 0; r < n_rows; ++r) {
-        const int32_t o = origin[r];
-        const int32_t len = row_ptr[o + 1] - row_ptr[o];
-        if (len == 0) continue;  // the arrays may be null when nnz == 0
-        std::memcpy(col_idx_out + row_ptr_out[r], col_idx + row_ptr[o],
-                    sizeof(int32_t) * static_cast<size_t>(len));
-        std::memcpy(val_out + row_ptr_out[r], val + row_ptr[o], sizeof(float) * static_cast<size_t>(len));
-    }
+    row_ptr_out[0] = 0;
+    parallel_for(T, [&](int t) {
+        int64_t acc = part[static_cast<size_t>(t)];
+        for (int32_t r = lo(t); r < lo(t + 1); ++r) {
+            acc += row_ptr[origin[r] + 1] - row_ptr[origin[r]];
+            row_ptr_out[r + 1] = static_cast<int32_t>(acc);
+        }
+    });
+
+    // 5. Row copies, each row keeping its entry order.  The degrees ascend,
+    //    so the chunks are cut at equal shares of the nonzeros, not rows.
+    const auto nz_lo = [&](int t) {
+        const int64_t target = nnz * t / T;
+        return static_cast<int32_t>(
+            std::lower_bound(row_ptr_out, row_ptr_out + n_rows, target) - row_ptr_out);
+    };
+    parallel_for(T, [&](int t) {
+        const int32_t end = t + 1 == T ? n_rows : nz_lo(t + 1);
+        for (int32_t r = t == 0 ? 0 : nz_lo(t); r < end; ++r) {
+            const int32_t o = origin[r];
+            const int32_t len = row_ptr[o + 1] - row_ptr[o];
+            if (len == 0) continue;  // the arrays may be null when nnz == 0
+            std::memcpy(col_idx_out + row_ptr_out[r], col_idx + row_ptr[o],
+                        sizeof(int32_t) * static_cast<size_t>(len));
+            std::memcpy(val_out + row_ptr_out[r], val + row_ptr[o],
+                        sizeof(float) * static_cast<size_t>(len));
+        }
+    });
     return CWLB_OK;
 }
 

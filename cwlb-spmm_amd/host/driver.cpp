@@ -3,6 +3,7 @@
 #include <algorithm>
 #include <cctype>
 #include <cstdint>
+#include <cstdlib>
 #include <iomanip>
 #include <iostream>
 #include <limits>
@@ -180,6 +181,27 @@ SingleSResult run_single_s(cwlb::Device& queue, const CSR_Order& csr,
     d_o.upload(csr.Origin_local);
     d_h.upload(features.data(), static_cast<std::size_t>(features.size()));
     d_t.upload(cwlb::host::as_c_tasks(tasks), tasks.size());
+
+    // The launch schedule for this graph and S, timed once before the timed
+    // launches like the S search itself (cwlb_ctx_tune_schedule), unless
+    // CWLB_TUNE_SCHEDULE=0 keeps the automatic schedule.  Both start from
+    // the automatic schedule in task order, so every S is treated alike.
+    cwlb::check(cwlb_ctx_set_schedule(queue.ctx(), 0, 0), "cwlb_ctx_set_schedule");
+    cwlb::check(cwlb_ctx_set_locality(queue.ctx(), 0, 0), "cwlb_ctx_set_locality");
+    const char* tune_env = std::getenv("CWLB_TUNE_SCHEDULE");
+    const bool tune = !(tune_env && std::string(tune_env) == "0");
+    if (tune && !tasks.empty() && K > 0) {
+        int32_t m = 0, sl = 0, loc[2] = {0, 0};
+        cwlb::check(cwlb_ctx_tune_schedule(queue.ctx(), d_rp.get(), d_ci.get(), d_v.get(),
+                                           d_o.get(), static_cast<int32_t>(rows),
+                                           static_cast<int64_t>(nnz), d_h.get(),
+                                           static_cast<int64_t>(features.rows()),
+                                           static_cast<int32_t>(K), d_t.get(),
+                                           static_cast<int64_t>(tasks.size()), d_c.get(), 3, &m,
+                                           &sl, loc),
+                    "cwlb_ctx_tune_schedule");
+        result.schedule = {m, sl, loc[0], loc[1]};
+    }
 
     const std::string device_name = queue.name();
     double accumulated = 0.0;

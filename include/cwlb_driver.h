@@ -68,6 +68,9 @@ struct SingleSResult {
     double average_us = 0.0;
     std::vector<double> timed_samples_us;
     Defined::RowMajorMatrixXf output;
+    // Launch schedule the timed launches ran with: tasks per wave, feature
+    // slices, run order, XCD placement (all 0 = the automatic schedule).
+    std::array<int, 4> schedule{};
 };
 
 // Builds the tasks for S (on the GPU, identical to the host partition), then
@@ -77,6 +80,10 @@ struct SingleSResult {
 // when K exceeds the device's maximum work-group size.  The reordered CSR
 // and H are uploaded once and stay on the device across the launches (the
 // reference re-copies them every launch; its timing excludes the copies).
+// Before the timed launches the launch schedule is tuned once for this S
+// (cwlb_ctx_tune_schedule, untimed; the environment variable
+// CWLB_TUNE_SCHEDULE=0 keeps the automatic schedule instead).  The schedule
+// stays set on the device afterwards.
 SingleSResult run_single_s(cwlb::Device& queue, const CSR_Order& sorted_csr,
                            const Defined::RowMajorMatrixXf& features, int feature_dim,
                            const SpmmCostParams& costs, int s, bool retain_timed_samples = false);

@@ -17,7 +17,7 @@
 //   spmm ORDER H ROWS K TASKS OUT      spmmKernel or, for K > 1024,
 //                                      spmmKernelLargeKFallback (prints time)
 //   spmm-large ORDER H ROWS K TASKS OUT   spmmKernelLargeKFallback
-//   run-single-s ORDER H ROWS K CC CL CS CA S OUT   run_single_s (prints average)
+//   run-single-s ORDER H ROWS K CC CL CS CA S OUT   run_single_s (prints average, schedule)
 //   load DIR NAME                      loadDatasetToCSR from working directory DIR
 //                                      (prints V E, then offsets and columns)
 //   features ROWS COLS OUT             deterministic_features
@@ -309,7 +309,9 @@ int run(int argc, char** argv)
         cwlb::Device q(0);
         const SingleSResult r = run_single_s(q, o, H, static_cast<int>(H.cols()), c, std::stoi(argv[10]), true);
         std::cout << "average " << r.average_us << " tasks " << r.task_count << " samples "
-                  << r.timed_samples_us.size() << " capacity " << r.capacity << "\n";
+                  << r.timed_samples_us.size() << " capacity " << r.capacity << " schedule "
+                  << r.schedule[0] << ',' << r.schedule[1] << ',' << r.schedule[2] << ','
+                  << r.schedule[3] << "\n";
         write_dense(argv[11], r.output);
     } else if (cmd == "load") {
         need(2);

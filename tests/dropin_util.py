@@ -18,11 +18,11 @@ class ProbeError(Exception):
         self.msg = msg
 
 
-def probe(*args, cwd=None, timeout=300):
+def probe(*args, cwd=None, timeout=300, env=None):
     if not os.path.exists(PROBE):
         raise RuntimeError(f"{PROBE} missing: build with __graft_entry__.build()")
     r = subprocess.run([PROBE, *map(str, args)], capture_output=True, text=True, cwd=cwd,
-                       timeout=timeout)
+                       timeout=timeout, env=None if env is None else {**os.environ, **env})
     out = r.stdout
     if r.returncode == 3:
         line = [ln for ln in out.splitlines() if "EXC " in ln][-1]

@@ -198,7 +198,11 @@ def test_dropin_degenerate_calls(tmp_path):
     assert e.value.kind == "invalid_argument"
 
 
-def test_dropin_run_single_s(tmp_path):
+@pytest.mark.parametrize("tune", ["1", "0"], ids=["tuned", "automatic"])
+def test_dropin_run_single_s(tmp_path, tune):
+    """run_single_s: 50 timed launches after 20 warm-ups, the reference's
+    tasks, the oracle's features; the launch schedule tuned first unless
+    CWLB_TUNE_SCHEDULE=0."""
     g = workloads.small(4, seed=6)
     K, S = 128, 16
     order = capi.reorder_by_degree(g.row_ptr, g.col_idx, g.val)
@@ -206,9 +210,17 @@ def test_dropin_run_single_s(tmp_path):
     write_order(tmp_path / "ord", *order)
     write_f32(tmp_path / "H", H)
     out = probe("run-single-s", tmp_path / "ord", tmp_path / "H", g.n, K, *SKEWED_COSTS, S,
-                tmp_path / "C").split()
-    rec = dict(zip(out[::2], out[1::2]))
+                tmp_path / "C", env={"CWLB_TUNE_SCHEDULE": tune})
+    last = out.strip().splitlines()[-1].split()
+    rec = dict(zip(last[::2], last[1::2]))
     assert float(rec["average"]) > 0 and rec["samples"] == "50"
+    m, sl, run_order, xcd = map(int, rec["schedule"].split(","))
+    if tune == "0":
+        assert (m, sl, run_order, xcd) == (0, 0, 0, 0)
+    else:
+        assert m in (0, 2, 4, 8, 16, 32, 64) and sl in (0, 1, 2, 4)
+        assert (run_order, xcd) in ((0, 0), (2, 1), (2, 2))
+    assert len([ln for ln in out.splitlines() if ln.startswith("[Iteration ")]) == 50
     cap = capi.capacity_from_s(S, SKEWED_COSTS)
     tasks = oracle.partition(order[1], SKEWED_COSTS, cap)
     assert int(rec["tasks"]) == len(tasks)

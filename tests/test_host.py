@@ -100,6 +100,24 @@ def test_reorder_bit_exact(cfg):
         assert np.array_equal(x, y)
 
 
+def test_reorder_threads_bit_exact(rng):
+    """A graph large enough for the threaded reordering (several row chunks,
+    chunks of the copies cut by nonzeros) with empty rows, runs of equal
+    degrees across chunk boundaries and rows at and above the 65,536-degree
+    histogram limit: identical to the oracle and to a stable argsort."""
+    n = 600_000
+    deg = rng.choice([0, 0, 1, 2, 3, 5, 8, 40], n).astype(np.int64)
+    deg[rng.integers(0, n, 6)] = [65535, 65536, 65537, 100000, 65536, 70000]
+    rp = np.concatenate([[0], np.cumsum(deg)]).astype(np.int32)
+    ci = rng.integers(0, n, rp[-1]).astype(np.int32)
+    val = rng.standard_normal(rp[-1]).astype(np.float32)
+    a = capi.reorder_by_degree(rp, ci, val)
+    b = oracle.reorder_by_degree(rp, ci, val)
+    for x, y in zip(a, b):
+        assert np.array_equal(x, y)
+    assert np.array_equal(a[0], np.argsort(deg, kind="stable"))
+
+
 def test_reorder_rejects_bad_csr():
     with pytest.raises(capi.CwlbError) as e:
         capi.reorder_by_degree(np.array([0, 5, 3], np.int32), np.zeros(5, np.int32),
