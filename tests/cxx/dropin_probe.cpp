@@ -207,12 +207,21 @@ std::vector<ParallelDataWeighted> partition_emulated(const std::vector<int>& rp,
         cnt[static_cast<std::size_t>(v)] = static_cast<int>(em.count);
         if (overrun) throw std::runtime_error("partition-emul: scan overrun");
     }
-    while (J.back()[0] != n) {
+    // As on the GPU: L levels with 2^(L-1) >= V, then the first level whose
+    // jump from A(0) reaches the end (which L levels must contain).
+    int L = 1;
+    while ((1LL << (L - 1)) < V) ++L;
+    while (static_cast<int>(J.size()) < L) {
         const std::vector<int>& a = J.back();
         std::vector<int> b(a.size());
         for (std::size_t v = 0; v < a.size(); ++v) b[v] = a[static_cast<std::size_t>(a[v])];
         J.push_back(std::move(b));
     }
+    int levels = 0;
+    for (int k = 0; k < L && levels == 0; ++k)
+        if (J[static_cast<std::size_t>(k)][0] == n) levels = k + 1;
+    if (levels == 0) throw std::runtime_error("partition-emul: chain too long");
+    J.resize(static_cast<std::size_t>(levels));
     const long long len = 1LL << (J.size() - 1);
     std::vector<int> chain(static_cast<std::size_t>(len), 0);
     for (int j = static_cast<int>(J.size()) - 2; j >= 0; --j) {
