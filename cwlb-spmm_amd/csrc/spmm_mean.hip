@@ -45,6 +45,8 @@ namespace {
 
 constexpr int kWaves = 4;
 constexpr int kBlock = 64 * kWaves;
+// A launch holds fewer than 2^32 work-items.
+constexpr long long kMaxGridBlocks = (1ll << 32) / kBlock - 8;
 
 typedef float f2 __attribute__((ext_vector_type(2)));
 typedef float f4 __attribute__((ext_vector_type(4)));
@@ -762,16 +764,21 @@ Plan make_plan(const cwlb_ctx* ctx, const SpmmArgs& a, bool per_task)
             p.M = static_cast<int>(std::max<long long>(1, std::min({m_par, m_rows, 64ll})));
         }
     }
-    p.runs = (a.n_tasks + p.M - 1) / p.M;
-    p.blocks = (p.runs + kWaves - 1) / kWaves;
     const bool contiguous = !per_task && ctx->sched_xcd == 2;
-    if (contiguous) {
-        const long long P = 8 / p.sl;
-        p.chunk = (p.blocks + P - 1) / P;
-        p.grid = p.chunk * 8;
-    } else {
-        p.chunk = 0;
-        p.grid = p.sl == 1 ? p.blocks : (p.blocks * p.sl + 7) / 8 * 8;
+    for (;;) {
+        p.runs = (a.n_tasks + p.M - 1) / p.M;
+        p.blocks = (p.runs + kWaves - 1) / kWaves;
+        if (contiguous) {
+            const long long P = 8 / p.sl;
+            p.chunk = (p.blocks + P - 1) / P;
+            p.grid = p.chunk * 8;
+        } else {
+            p.chunk = 0;
+            p.grid = p.sl == 1 ? p.blocks : (p.blocks * p.sl + 7) / 8 * 8;
+        }
+        // An automatic run length grows until the grid fits one launch.
+        if (p.grid <= kMaxGridBlocks || per_task || ctx->sched_tasks_per_wave > 0) break;
+        p.M *= 2;
     }
     p.ordered = !per_task && ctx->sched_order == 2 && p.runs > 1;
     p.order = nullptr;
@@ -785,6 +792,11 @@ cwlb_status launch_spmm_mean(cwlb_ctx* ctx, const SpmmArgs& a, bool zero_all, bo
 {
     hipStream_t st = ctx->stream;
     (void)hipGetLastError();  // report only the launches below
+    Plan p = make_plan(ctx, a, per_task);
+    if (p.grid > kMaxGridBlocks && a.n_tasks > 0 && a.K > 0)
+        return fail(CWLB_UNSUPPORTED,
+                    "spmm: too many runs for one launch (more than 2^32 work-items); use more "
+                    "tasks per wave (cwlb_ctx_set_schedule) or a larger S");
     if (record_events) CWLB_HIP_TRY(hipEventRecord(ctx->ev[0], st));
     const long long total = static_cast<long long>(a.n_rows) * a.K;
     if (zero_all) {
@@ -794,7 +806,6 @@ cwlb_status launch_spmm_mean(cwlb_ctx* ctx, const SpmmArgs& a, bool zero_all, bo
         hipLaunchKernelGGL(fill_zero, dim3(blocks), dim3(kBlock), 0, st, a.C,
                            std::max<long long>(total, 0), ctx->d_status);
     }
-    Plan p = make_plan(ctx, a, per_task);
     if (p.ordered && a.n_tasks > 0 && a.K > 0) {
         const cwlb_status s = build_run_order(ctx, a, p.M, p.runs, &p.order);
         if (s != CWLB_OK) return s;

@@ -388,6 +388,34 @@ def test_zero_output_flag_with_partial_cover(gpu_ctx):
     check(got, ref32)
 
 
+def test_launch_grid_limit(gpu_ctx):
+    """70M empty tasks: one task per wave (or a fixed run length of 1) would
+    need more than 2^32 work-items and is refused before any launch; the
+    automatic run length fits."""
+    torch = torch_mod()
+    T = 70_000_000
+    tasks = torch.zeros(T * 4, dtype=torch.int32, device="cuda")
+    rp = dev(np.zeros(2, np.int32))
+    ci, val = dev(np.zeros(1, np.int32)), dev(np.zeros(1, np.float32))
+    origin = dev(np.zeros(1, np.int32))
+    H = torch.ones((1, 32), dtype=torch.float32, device="cuda")
+    C = torch.full((1, 32), 7.0, dtype=torch.float32, device="cuda")
+    args = (rp, ci, val, origin, 1, 0, H, 1, 32, tasks, T, C)
+    with pytest.raises(capi.CwlbError) as e:
+        gpu_ctx.spmm(*args, flags=capi.PER_TASK)
+    assert e.value.status == capi.UNSUPPORTED
+    gpu_ctx.set_schedule(1, 1)
+    try:
+        with pytest.raises(capi.CwlbError) as e:
+            gpu_ctx.spmm(*args)
+        assert e.value.status == capi.UNSUPPORTED
+    finally:
+        gpu_ctx.set_schedule(0, 0)
+    assert torch.all(C == 7.0)  # nothing ran
+    gpu_ctx.spmm(*args, flags=capi.ZERO_OUTPUT)
+    assert torch.all(C == 0.0)
+
+
 def test_no_tasks_and_zero_k(gpu_ctx):
     g = workloads.small(1, seed=2)
     H = synth.features(g.n, 32, 3)
