@@ -29,6 +29,7 @@ sys.path.insert(0, os.path.join(ROOT, "cwlb-spmm_amd"))
 METRIC = "SpMM GFLOP/s (2·nnz·K/t) + achieved HBM GB/s vs peak, FP32 mean agg"
 HBM_PEAK_GBS = 8000.0
 COST_FILE = os.path.join(ROOT, "cwlb-spmm_amd", "resources", "spmm_costs_gfx950.txt")
+GOLDEN = os.path.join(ROOT, "tests", "golden", "partition_golden.json")
 # Committed rocprofv3 PMC summaries per workload configuration (traffic per
 # aggregation launch, FETCH_SIZE + WRITE_SIZE scaled by a known-size copy).
 PMC_SUMMARY = {
@@ -54,6 +55,28 @@ def measured_traffic(cfg, S):
     found = dict(re.findall(r"traffic_bytes_per_launch(?:\[S=(\d+)\])?:\s*([0-9.eE+]+)", text))
     value = found.get(str(S), found.get(""))
     return float(value) if value is not None else None
+
+
+def reference_partition_match(cfg, S, costs, tasks):
+    """Whether the task list equals, by SHA-256, the one the reference's own
+    costWeightedTaskPartitioning produced for this graph, S and cost vector
+    (tests/golden/partition_golden.json); None when the fixture has no such
+    case."""
+    import hashlib
+
+    import numpy as np
+    try:
+        golden = json.load(open(GOLDEN))
+    except OSError:
+        return None
+    rec = golden["full"].get(str(cfg))
+    if rec is None:
+        return None
+    for p in rec["partitions"]:
+        if p["S"] == S and golden["costs"][p["costs"]] == list(costs):
+            digest = hashlib.sha256(np.ascontiguousarray(tasks).astype("<i4").tobytes())
+            return digest.hexdigest() == p["tasks_sha256"]
+    return None
 
 
 def preprocessing_times(ctx, g, rp, costs, S, tasks, reorder_host_ms):
@@ -185,6 +208,7 @@ def main():
     S, auto_us, tasks, d_t = best
     T = len(tasks)
     prep = preprocessing_times(ctx, g, rp, costs, S, tasks, reorder_host_ms)
+    prep["tasks_match_reference_fixture"] = reference_partition_match(cfg, S, costs, tasks)
     log(f"preprocessing: {prep}")
     # Launch schedule for this graph and S: measured once, like the S search
     # (cwlb_ctx_tune_schedule; 0, 0 = the automatic choice won).

@@ -348,14 +348,23 @@ def test_device_partition_small(gpu_ctx, cfg):
 
 @pytest.mark.parametrize("cfg", [2, 3, 4, 5])
 def test_device_partition_full(gpu_ctx, cfg):
-    """Full-size graphs at the three wave-based S with the gfx950 costs:
-    task-for-task identical to the host partition."""
+    """Full-size graphs at the three wave-based S (and the mesh's S sweep)
+    with the gfx950 costs: task-for-task identical to the host partition,
+    and SHA-256-identical to the reference partition's fixture
+    (tests/golden/partition_golden.json)."""
     import time
+    from test_golden import GOLDEN, sha
+    rec = GOLDEN["full"][str(cfg)]
     g = workloads.graph(cfg)
+    d_origin, d_rp, _, _ = reorder_on_device(gpu_ctx, g.row_ptr, g.col_idx, g.val)
+    assert sha(d_origin) == rec["origin_sha256"] and sha(d_rp) == rec["sorted_row_ptr_sha256"]
     _, rp, _, _ = capi.reorder_by_degree(g.row_ptr, g.col_idx, g.val)
-    costs = (0.004519, 0.015617, 0.010667, 0.540499)
-    for S in workloads.candidate_s(g.nnz, 256):
+    assert np.array_equal(rp, d_rp)
+    costs = GOLDEN["costs"]["gfx950"]
+    for p in rec["partitions"]:
+        S = p["S"]
         cap = capi.capacity_from_s(S, costs)
+        assert cap == float.fromhex(p["capacity"])
         t0 = time.perf_counter()
         got = device_partition(gpu_ctx, rp, costs, cap)
         t1 = time.perf_counter()
@@ -364,6 +373,26 @@ def test_device_partition_full(gpu_ctx, cfg):
         print(f"cfg={cfg} S={S} T={len(exp)} device {1e3 * (t1 - t0):.1f} ms (two calls) "
               f"host {1e3 * (t2 - t1):.1f} ms", flush=True)
         assert np.array_equal(got, exp)
+        assert (len(got), sha(got)) == (p["n_tasks"], p["tasks_sha256"])
+
+
+def test_device_partition_random_fixture(gpu_ctx):
+    """The reference partition's random fixture cases (sorted and unsorted
+    degree sequences, assorted costs) on the GPU partition; cases whose
+    costs have no row bound are refused and stay with the host."""
+    from test_golden import GOLDEN, random_case, sha
+    ran = 0
+    for c in GOLDEN["random"]:
+        rp, costs, cap = random_case(c)
+        try:
+            got = device_partition(gpu_ctx, rp, costs, cap)
+        except capi.CwlbError as e:
+            assert e.status == capi.UNSUPPORTED
+            continue
+        assert (len(got), sha(got)) == (c["n_tasks"], c["tasks_sha256"]), c
+        ran += 1
+    print(f"random fixture cases on the GPU: {ran} of {len(GOLDEN['random'])}", flush=True)
+    assert ran >= 40
 
 
 def test_device_partition_random(gpu_ctx, rng):
