@@ -79,6 +79,29 @@ def reference_partition_match(cfg, S, costs, tasks):
     return None
 
 
+def segment_size_sweep(ctx, call, tune, dev, tasks_for, cfg, costs, S, trials):
+    """Aggregation kernel time at segment size S: mean of `trials`
+    event-timed launches with the automatic schedule, then with the schedule
+    cwlb_ctx_tune_schedule keeps for this S (outside the timed launches)."""
+    import numpy as np
+    tk = tasks_for(S)
+    d_t = dev(tk.reshape(-1))
+    ctx.set_schedule(0, 0)
+    ctx.set_locality(0, 0)
+    for _ in range(3):
+        call(d_t, len(tk), False)
+    auto_us = float(np.mean([call(d_t, len(tk), True).main_us for _ in range(trials)]))
+    m, sl, (order, xcd) = tune(d_t, len(tk))
+    for _ in range(3):
+        call(d_t, len(tk), False)
+    tuned_us = float(np.mean([call(d_t, len(tk), True).main_us for _ in range(trials)]))
+    return {"S": S, "tasks": int(len(tk)), "automatic_us": round(auto_us, 1),
+            "tuned_us": round(tuned_us, 1),
+            "schedule": {"tasks_per_wave": m, "feature_slices": sl, "run_order": order,
+                         "xcd_blocks": xcd},
+            "tasks_match_reference_fixture": reference_partition_match(cfg, S, costs, tk)}
+
+
 def preprocessing_times(ctx, g, rp, costs, S, tasks, reorder_host_ms):
     """Wall times (ms) of the degree reordering and the partition at S, on
     the host and on the GPU (outside the timed region; results checked
@@ -142,6 +165,10 @@ def main():
                     help="fixed run order (cwlb_ctx_set_locality: 1 task order, 2 by output row)")
     ap.add_argument("--xcd-blocks", type=int, default=0,
                     help="fixed XCD placement (1 interleaved, 2 contiguous)")
+    ap.add_argument("--s-sweep", default=None,
+                    help="comma-separated segment sizes timed after the measured step, each "
+                         "with the automatic and the tuned schedule (default: 32,64,128,256,512 "
+                         "for the mesh workload, none otherwise; '' for none)")
     ap.add_argument("--no-tune", action="store_true",
                     help="keep the automatic launch schedule (no cwlb_ctx_tune_schedule)")
     ap.add_argument("--no-host-call", action="store_true",
@@ -192,6 +219,10 @@ def main():
     def call(d_t, n_t, timed):
         return ctx.spmm(d_rp, d_ci, d_v, d_o, g.n, g.nnz, H, g.n, K, d_t, n_t, C, timed=timed,
                         large_k=large_k)
+
+    def tune(d_t, n_t):
+        return ctx.tune_schedule(d_rp, d_ci, d_v, d_o, g.n, g.nnz, H, g.n, K, d_t, n_t, C,
+                                 trials=3, locality=True)
 
     # S: the best of the three wave-based candidates (main.cpp:534-577), or fixed.
     cands = [args.s] if args.s else workloads.candidate_s(g.nnz, info.compute_units)
@@ -271,6 +302,15 @@ def main():
         log(f"copy probe: {nb} bytes read and written")
         del src, dst
 
+    sweep_arg = args.s_sweep if args.s_sweep is not None else (
+        "32,64,128,256,512" if cfg == 5 and not args.k else "")
+    s_sweep = [segment_size_sweep(ctx, call, tune, dev, tasks_for, cfg, costs, int(x), trials=10)
+               for x in sweep_arg.split(",") if x.strip()]
+    if s_sweep:
+        log(f"S sweep: {s_sweep}")
+        ctx.set_schedule(0, 0)
+        ctx.set_locality(0, 0)
+
     flops = 2.0 * g.nnz * K
     gflops = flops / (ms_per_step * 1e-3) / 1e9
     b_alg = workloads.algorithmic_bytes(g.n, g.nnz, K, T)
@@ -325,6 +365,7 @@ def main():
                    "host_pointer_call_ms": None if host_call_ms is None else round(host_call_ms, 1),
                    "preprocessing": prep,
                    "schedule": schedule,
+                   **({"s_sweep": s_sweep} if s_sweep else {}),
                    "algorithmic_bytes": b_alg},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
