@@ -168,7 +168,7 @@ def main():
     ap.add_argument("--s-sweep", default=None,
                     help="comma-separated segment sizes timed after the measured step, each "
                          "with the automatic and the tuned schedule (default: 32,64,128,256,512 "
-                         "for the mesh workload, none otherwise; '' for none)")
+                         "for the mesh workload, none otherwise; 'none' for none)")
     ap.add_argument("--no-tune", action="store_true",
                     help="keep the automatic launch schedule (no cwlb_ctx_tune_schedule)")
     ap.add_argument("--no-host-call", action="store_true",
@@ -305,7 +305,7 @@ def main():
     sweep_arg = args.s_sweep if args.s_sweep is not None else (
         "32,64,128,256,512" if cfg == 5 and not args.k else "")
     s_sweep = [segment_size_sweep(ctx, call, tune, dev, tasks_for, cfg, costs, int(x), trials=10)
-               for x in sweep_arg.split(",") if x.strip()]
+               for x in sweep_arg.split(",") if x.strip() and x.strip() != "none"]
     if s_sweep:
         log(f"S sweep: {s_sweep}")
         ctx.set_schedule(0, 0)
