@@ -1,8 +1,10 @@
 // C ABI of libcwlb: contexts, errors and the SpMM entry points.
 #include <algorithm>
+#include <atomic>
 #include <cstdio>
 #include <cstring>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "internal.h"
@@ -94,6 +96,98 @@ cwlb_status run_spmm(cwlb_ctx* ctx, const SpmmArgs& a, uint32_t flags, cwlb_timi
     return CWLB_OK;
 }
 
+// fn(begin, end) over [0, n) split into contiguous parts, on up to 8 host
+// threads (one per 8 MiB of work or so), the caller's thread included.
+template <class Fn>
+void parallel_ranges(size_t n, size_t grain, Fn fn)
+{
+    const unsigned hw = std::max(1u, std::thread::hardware_concurrency());
+    const size_t T = std::max<size_t>(1, std::min<size_t>({size_t{8}, hw, n / grain}));
+    if (T == 1) {
+        fn(size_t{0}, n);
+        return;
+    }
+    std::vector<std::thread> pool;
+    pool.reserve(T - 1);
+    for (size_t t = 1; t < T; ++t)
+        pool.emplace_back([&, t] { fn(n * t / T, n * (t + 1) / T); });
+    fn(size_t{0}, n / T);
+    for (auto& th : pool) th.join();
+}
+
+void parallel_copy(void* dst, const void* src, size_t bytes)
+{
+    parallel_ranges(bytes, size_t{8} << 20, [&](size_t b, size_t e) {
+        std::memcpy(static_cast<char*>(dst) + b, static_cast<const char*>(src) + b, e - b);
+    });
+}
+
+// Host-pointer transfers through the context's two pinned staging buffers:
+// while the DMA engine moves one buffer, the host threads fill (or drain)
+// the other.
+constexpr size_t kStageBytes = size_t{64} << 20;
+
+cwlb_status ensure_staging(cwlb_ctx* ctx)
+{
+    for (int b = 0; b < 2; ++b) {
+        if (!ctx->h_stage[b])
+            CWLB_HIP_TRY(hipHostMalloc(&ctx->h_stage[b], kStageBytes, hipHostMallocDefault));
+        if (!ctx->stage_ev[b]) {
+            CWLB_HIP_TRY(hipEventCreateWithFlags(&ctx->stage_ev[b], hipEventDisableTiming));
+            CWLB_HIP_TRY(hipEventRecord(ctx->stage_ev[b], ctx->stream));
+        }
+    }
+    return CWLB_OK;
+}
+
+struct Stager {
+    cwlb_ctx* ctx;
+    unsigned next = 0;  // staging buffer of the next chunk
+
+    cwlb_status to_device(void* d_dst, const void* h_src, size_t bytes)
+    {
+        for (size_t off = 0; off < bytes; off += kStageBytes) {
+            const size_t n = std::min(kStageBytes, bytes - off);
+            const unsigned b = next++ & 1u;
+            CWLB_HIP_TRY(hipEventSynchronize(ctx->stage_ev[b]));  // its last DMA is done
+            parallel_copy(ctx->h_stage[b], static_cast<const char*>(h_src) + off, n);
+            CWLB_HIP_TRY(hipMemcpyAsync(static_cast<char*>(d_dst) + off, ctx->h_stage[b], n,
+                                        hipMemcpyHostToDevice, ctx->stream));
+            CWLB_HIP_TRY(hipEventRecord(ctx->stage_ev[b], ctx->stream));
+        }
+        return CWLB_OK;
+    }
+
+    cwlb_status to_host(void* h_dst, const void* d_src, size_t bytes)
+    {
+        size_t prev_off = 0, prev_n = 0;
+        unsigned prev_b = 0;
+        bool pending = false;
+        for (size_t off = 0; off < bytes; off += kStageBytes) {
+            const size_t n = std::min(kStageBytes, bytes - off);
+            const unsigned b = next++ & 1u;
+            // Buffer b was drained (or only read by a finished upload).
+            CWLB_HIP_TRY(hipEventSynchronize(ctx->stage_ev[b]));
+            CWLB_HIP_TRY(hipMemcpyAsync(ctx->h_stage[b], static_cast<const char*>(d_src) + off,
+                                        n, hipMemcpyDeviceToHost, ctx->stream));
+            CWLB_HIP_TRY(hipEventRecord(ctx->stage_ev[b], ctx->stream));
+            if (pending) {
+                CWLB_HIP_TRY(hipEventSynchronize(ctx->stage_ev[prev_b]));
+                parallel_copy(static_cast<char*>(h_dst) + prev_off, ctx->h_stage[prev_b], prev_n);
+            }
+            prev_off = off;
+            prev_n = n;
+            prev_b = b;
+            pending = true;
+        }
+        if (pending) {
+            CWLB_HIP_TRY(hipEventSynchronize(ctx->stage_ev[prev_b]));
+            parallel_copy(static_cast<char*>(h_dst) + prev_off, ctx->h_stage[prev_b], prev_n);
+        }
+        return CWLB_OK;
+    }
+};
+
 template <class T>
 struct DevBuf {
     T* p = nullptr;
@@ -165,6 +259,11 @@ cwlb_status cwlb_ctx_destroy(cwlb_ctx* ctx)
     for (void* p : {static_cast<void*>(ctx->d_run_keys), static_cast<void*>(ctx->d_run_keys_sorted),
                     static_cast<void*>(ctx->d_run_order), ctx->d_sort_temp})
         if (p) (void)hipFree(p);
+    for (int b = 0; b < 2; ++b) {
+        if (ctx->stage_ev[b]) (void)hipEventSynchronize(ctx->stage_ev[b]);
+        if (ctx->stage_ev[b]) (void)hipEventDestroy(ctx->stage_ev[b]);
+        if (ctx->h_stage[b]) (void)hipHostFree(ctx->h_stage[b]);
+    }
     delete ctx;
     return CWLB_OK;
 }
@@ -367,12 +466,21 @@ cwlb_status cwlb_spmm_mean_f32_host(cwlb_ctx* ctx, const int32_t* row_ptr,
     // Host-side validation keeps every device access in bounds.
     if (row_ptr[0] < 0 || row_ptr[n_rows] > nnz)
         return fail(CWLB_INVALID_ARG, "spmm: row_ptr outside [0, nnz]");
-    for (int32_t r = 0; r < n_rows; ++r)
-        if (row_ptr[r + 1] < row_ptr[r])
-            return fail(CWLB_INVALID_ARG, "spmm: row_ptr is not non-decreasing");
-    for (int64_t j = 0; j < nnz; ++j)
-        if (col_idx[j] < 0 || col_idx[j] >= h_rows)
-            return fail(CWLB_INVALID_ARG, "spmm: column index outside [0, h_rows)");
+    std::atomic<bool> bad_rp{false}, bad_ci{false};
+    parallel_ranges(static_cast<size_t>(n_rows), size_t{1} << 20, [&](size_t b, size_t e) {
+        bool bad = false;
+        for (size_t r = b; r < e; ++r) bad |= row_ptr[r + 1] < row_ptr[r];
+        if (bad) bad_rp = true;
+    });
+    if (bad_rp) return fail(CWLB_INVALID_ARG, "spmm: row_ptr is not non-decreasing");
+    parallel_ranges(static_cast<size_t>(nnz), size_t{1} << 21, [&](size_t b, size_t e) {
+        bool bad = false;
+        for (size_t j = b; j < e; ++j) bad |= col_idx[j] < 0 || col_idx[j] >= h_rows;
+        if (bad) bad_ci = true;
+    });
+    if (bad_ci) return fail(CWLB_INVALID_ARG, "spmm: column index outside [0, h_rows)");
+    cwlb_status s = ensure_staging(ctx);
+    if (s != CWLB_OK) return s;
     DevBuf<int32_t> d_rp, d_ci, d_or;
     DevBuf<float> d_val, d_H, d_C;
     DevBuf<cwlb_task> d_t;
@@ -384,22 +492,25 @@ cwlb_status cwlb_spmm_mean_f32_host(cwlb_ctx* ctx, const int32_t* row_ptr,
     CWLB_HIP_TRY(d_C.alloc(out_elems));
     CWLB_HIP_TRY(d_t.alloc(static_cast<size_t>(n_tasks)));
     hipStream_t st = ctx->stream;
-    CWLB_HIP_TRY(hipMemcpyAsync(d_rp.p, row_ptr, sizeof(int32_t) * (n_rows + 1), hipMemcpyHostToDevice, st));
-    if (nnz) {
-        CWLB_HIP_TRY(hipMemcpyAsync(d_ci.p, col_idx, sizeof(int32_t) * nnz, hipMemcpyHostToDevice, st));
-        CWLB_HIP_TRY(hipMemcpyAsync(d_val.p, val, sizeof(float) * nnz, hipMemcpyHostToDevice, st));
+    Stager io{ctx};
+    s = io.to_device(d_rp.p, row_ptr, sizeof(int32_t) * (n_rows + 1));
+    if (s == CWLB_OK) s = io.to_device(d_ci.p, col_idx, sizeof(int32_t) * nnz);
+    if (s == CWLB_OK) s = io.to_device(d_val.p, val, sizeof(float) * nnz);
+    if (s == CWLB_OK) s = io.to_device(d_or.p, origin, sizeof(int32_t) * n_rows);
+    if (s == CWLB_OK) s = io.to_device(d_H.p, H, sizeof(float) * h_rows * K);
+    if (s == CWLB_OK) s = io.to_device(d_t.p, tasks, sizeof(cwlb_task) * n_tasks);
+    if (s != CWLB_OK) {
+        (void)hipStreamSynchronize(st);  // no DMA may outlive the device buffers
+        return s;
     }
-    if (n_rows)
-        CWLB_HIP_TRY(hipMemcpyAsync(d_or.p, origin, sizeof(int32_t) * n_rows, hipMemcpyHostToDevice, st));
-    if (h_rows * K)
-        CWLB_HIP_TRY(hipMemcpyAsync(d_H.p, H, sizeof(float) * h_rows * K, hipMemcpyHostToDevice, st));
-    CWLB_HIP_TRY(hipMemcpyAsync(d_t.p, tasks, sizeof(cwlb_task) * n_tasks, hipMemcpyHostToDevice, st));
     SpmmArgs a{d_rp.p, d_ci.p, d_val.p, d_or.p, n_rows, nnz, d_H.p, h_rows, K, d_t.p, n_tasks, d_C.p};
     cwlb_timing local{};
-    cwlb_status s = run_spmm(ctx, a, CWLB_SPMM_ZERO_OUTPUT, &local);
-    if (s != CWLB_OK) return s;
-    if (out_elems)
-        CWLB_HIP_TRY(hipMemcpyAsync(C, d_C.p, sizeof(float) * out_elems, hipMemcpyDeviceToHost, st));
+    s = run_spmm(ctx, a, CWLB_SPMM_ZERO_OUTPUT, &local);
+    if (s == CWLB_OK) s = io.to_host(C, d_C.p, sizeof(float) * out_elems);
+    if (s != CWLB_OK) {
+        (void)hipStreamSynchronize(st);
+        return s;
+    }
     CWLB_HIP_TRY(hipStreamSynchronize(st));
     // The reference times the aggregation kernel only; C's clearing is the
     // host-side Zero() there.

@@ -45,6 +45,10 @@ struct cwlb_ctx {
     int order_M = 0;
     void* d_sort_temp = nullptr;
     size_t sort_temp_bytes = 0;
+    // Pinned host staging of the host-pointer entry point: two buffers used
+    // alternately, each with the event of the last transfer through it.
+    void* h_stage[2] = {nullptr, nullptr};
+    hipEvent_t stage_ev[2] = {nullptr, nullptr};
 };
 
 namespace cwlb {

@@ -460,6 +460,24 @@ def test_host_pointer_entry(gpu_ctx):
     assert t.main_us > 0
 
 
+def test_host_pointer_entry_multi_chunk(gpu_ctx):
+    """Inputs and output larger than one 64 MiB staging buffer (H and C of
+    about 160 MB each: several chunks through both buffers), then a small
+    call on the same context."""
+    g = workloads.small(2, seed=4)
+    K = 2048
+    H = synth.features(g.n, K, 6)
+    p = problem(g, SKEWED_COSTS, 32)
+    got, _ = gpu_ctx.spmm_host(p.row_ptr, p.col_idx, p.val, p.origin, H, p.tasks)
+    ref32 = oracle.spmm_mean_f32(p.row_ptr, p.col_idx, p.val, p.origin, H, p.tasks)
+    check(got, ref32)
+    g2 = workloads.small(1, seed=4)
+    H2 = synth.features(g2.n, 32, 6)
+    p2 = problem(g2, UNIT_COSTS, 8)
+    got2, _ = gpu_ctx.spmm_host(p2.row_ptr, p2.col_idx, p2.val, p2.origin, H2, p2.tasks)
+    check(got2, oracle.spmm_mean_f32(p2.row_ptr, p2.col_idx, p2.val, p2.origin, H2, p2.tasks))
+
+
 def test_repeat_runs_stable(gpu_ctx):
     """Full rows are written identically on every run; split rows within tolerance."""
     g = workloads.small(4, seed=4)
