@@ -366,7 +366,9 @@ def main():
                    "preprocessing": prep,
                    "schedule": schedule,
                    **({"s_sweep": s_sweep} if s_sweep else {}),
-                   "algorithmic_bytes": b_alg},
+                   "algorithmic_bytes": b_alg,
+                   # measured HBM-side traffic per launch / the same launch time
+                   "traffic_gbs": None if traffic is None else round(traffic / (main_us * 1e-6) / 1e9, 1)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic},
