@@ -250,6 +250,58 @@ def test_full_config_properties(gpu_ctx, cfg, per_task):
     print(f"cfg={cfg} total_us={t.total_us:.1f} zero_us={t.zero_us:.1f}", flush=True)
 
 
+@pytest.mark.parametrize("K", [1028, 2048])
+def test_full_chunglu_large_k_properties(gpu_ctx, K):
+    """The large-K entry (K above the 1,024-lane work-group limit) on the
+    full-size Chung-Lu graph (1M rows, 9.1M nonzeros; H and C of 4-8 GB):
+    all-ones features give exactly 1 (0 for empty rows) on rows no task
+    splits and stay within the rounding bound on split rows; with seeded
+    features, sampled rows (random and the 200 highest-degree) match the
+    fp64 closed form.  Checked on the device, without copying C back."""
+    torch = torch_mod()
+    g = workloads.graph(2)
+    S = workloads.candidate_s(g.nnz, 256)[2]
+    p = problem(g, SKEWED_COSTS, S)
+    print(f"K={K} n={g.n} nnz={g.nnz} S={S} tasks={len(p.tasks)}", flush=True)
+    d_rp, d_ci, d_v, d_o = dev(p.row_ptr), dev(p.col_idx), dev(p.val), dev(p.origin)
+    d_t = dev(np.ascontiguousarray(p.tasks, np.int32).reshape(-1))
+    C = torch.full((g.n, K), float("nan"), dtype=torch.float32, device="cuda")
+    ones = torch.ones((g.n, K), dtype=torch.float32, device="cuda")
+    gpu_ctx.spmm(d_rp, d_ci, d_v, d_o, g.n, g.nnz, ones, g.n, K, d_t, len(p.tasks), C,
+                 large_k=True)
+    del ones
+    touch = np.zeros(g.n, np.int64)
+    touch[p.origin] = tasks_per_row(p)
+    split = np.zeros(g.n, bool)
+    split[p.origin[split_rows(p)]] = True
+    deg = np.diff(g.row_ptr)
+    exact = torch.from_numpy(np.where(deg > 0, 1.0, 0.0).astype(np.float32)).cuda()
+    whole = torch.from_numpy(~split).cuda()
+    assert bool((C[whole] == exact[whole, None]).all().item())
+    bound = torch.from_numpy(((touch + 1) * 2.0**-23).astype(np.float32)).cuda()
+    sp = torch.from_numpy(split).cuda()
+    assert bool(((C[sp] - 1.0).abs() <= bound[sp, None]).all().item())
+    H = torch.empty((g.n, K), dtype=torch.float32, device="cuda")
+    gpu_ctx.fill_features(H, g.n, K, workloads.FEATURE_SEED)
+    C.fill_(float("nan"))
+    t = gpu_ctx.spmm(d_rp, d_ci, d_v, d_o, g.n, g.nnz, H, g.n, K, d_t, len(p.tasks), C,
+                     large_k=True)
+    assert not torch.isnan(C).any().item()
+    rng = np.random.default_rng(K)
+    rows = np.unique(np.concatenate([rng.integers(0, g.n, 300),
+                                     np.argsort(deg, kind="stable")[-200:]]))
+    got = C[torch.from_numpy(rows).cuda()].cpu().numpy()
+    for i, r in enumerate(rows):
+        lo, hi = g.row_ptr[r], g.row_ptr[r + 1]
+        exp = np.zeros(K)
+        if hi > lo:
+            cols = torch.from_numpy(g.col_idx[lo:hi].astype(np.int64)).cuda()
+            feats = H[cols].cpu().numpy().astype(np.float64)
+            exp = (g.val[lo:hi, None].astype(np.float64) * feats).sum(0) / (hi - lo)
+        np.testing.assert_allclose(got[i], exp, rtol=RTOL, atol=ATOL)
+    print(f"K={K} total_us={t.total_us:.1f}", flush=True)
+
+
 # ------------------------------------------------------------------ edge cases
 @pytest.mark.parametrize("K", [1, 2, 3, 4, 6, 12, 20, 36, 64, 100, 128, 192, 256, 260, 512, 600,
                                1000, 1024])
