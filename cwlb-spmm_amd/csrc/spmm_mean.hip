@@ -733,9 +733,12 @@ int pick_vec(const SpmmArgs& a)
 // Automatic schedule (the context's settings override each choice):
 //   * feature slices across XCDs only when the feature matrix is well beyond
 //     what the 256 MB Infinity Cache holds (>= 512 MB): then each XCD's L2
-//     caching one 128-byte slice of the hot rows pays; below that, slicing
-//     only multiplies the per-row work (measured: Chung-Lu K=64, H = 256 MB,
-//     10% slower with 2 slices; R-MAT K=128, H = 2 GB, 4-5% faster with 4);
+//     caching a slice of the hot rows pays; below that, slicing only
+//     multiplies the per-row work (measured: Chung-Lu K=64, H = 256 MB, 10%
+//     slower with 2 slices).  Slices of 32 to 128 floats are best: 2 slices
+//     up to K = 256, 4 slices up to K = 512 (measured on R-MAT, H = 2 to
+//     8.6 GB: K=128 2 slices 1.4% faster than 4, K=256 3.5% faster; K=512
+//     4 slices 2% faster than 2; K=192 2 slices 18% faster than 1);
 //   * tasks per wave M: the largest M that keeps at least 64 waves per CU
 //     (runs x slices) and at most ~256 rows per run (long runs of short rows
 //     serialise latency: the 16M-row mesh is 9% faster at 4 tasks per wave
@@ -751,8 +754,8 @@ Plan make_plan(const cwlb_ctx* ctx, const SpmmArgs& a, bool per_task)
         if (ctx->sched_slices > 0) {
             p.sl = ctx->sched_slices;
         } else if (h_bytes >= (512ll << 20)) {
-            if (a.K % 128 == 0 && a.K >= 128 && a.K <= 512) p.sl = 4;
-            else if (a.K % 64 == 0 && a.K >= 64 && a.K <= 256) p.sl = 2;
+            if (a.K % 64 == 0 && a.K >= 64 && a.K <= 256) p.sl = 2;
+            else if (a.K % 128 == 0 && a.K > 256 && a.K <= 512) p.sl = 4;
         }
         if (p.vec != 4 || a.K % (4 * p.sl) != 0) p.sl = 1;
         if (ctx->sched_tasks_per_wave > 0) {
