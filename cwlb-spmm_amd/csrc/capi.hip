@@ -127,25 +127,44 @@ void parallel_copy(void* dst, const void* src, size_t bytes)
 // the other.
 constexpr size_t kStageBytes = size_t{64} << 20;
 
-cwlb_status ensure_staging(cwlb_ctx* ctx)
+// True when both staging buffers and their events exist (allocated at the
+// first call).  Without them (pinned memory refused) the caller copies
+// directly from its pageable arrays.
+bool ensure_staging(cwlb_ctx* ctx)
 {
     for (int b = 0; b < 2; ++b) {
-        if (!ctx->h_stage[b])
-            CWLB_HIP_TRY(hipHostMalloc(&ctx->h_stage[b], kStageBytes, hipHostMallocDefault));
+        if (!ctx->h_stage[b] &&
+            hipHostMalloc(&ctx->h_stage[b], kStageBytes, hipHostMallocDefault) != hipSuccess) {
+            ctx->h_stage[b] = nullptr;
+            (void)hipGetLastError();
+            return false;
+        }
         if (!ctx->stage_ev[b]) {
-            CWLB_HIP_TRY(hipEventCreateWithFlags(&ctx->stage_ev[b], hipEventDisableTiming));
-            CWLB_HIP_TRY(hipEventRecord(ctx->stage_ev[b], ctx->stream));
+            if (hipEventCreateWithFlags(&ctx->stage_ev[b], hipEventDisableTiming) != hipSuccess ||
+                hipEventRecord(ctx->stage_ev[b], ctx->stream) != hipSuccess) {
+                if (ctx->stage_ev[b]) (void)hipEventDestroy(ctx->stage_ev[b]);
+                ctx->stage_ev[b] = nullptr;
+                (void)hipGetLastError();
+                return false;
+            }
         }
     }
-    return CWLB_OK;
+    return true;
 }
 
 struct Stager {
     cwlb_ctx* ctx;
+    bool direct;        // no pinned buffers: plain (pageable) copies
     unsigned next = 0;  // staging buffer of the next chunk
 
     cwlb_status to_device(void* d_dst, const void* h_src, size_t bytes)
     {
+        if (direct) {
+            if (bytes)
+                CWLB_HIP_TRY(hipMemcpyAsync(d_dst, h_src, bytes, hipMemcpyHostToDevice,
+                                            ctx->stream));
+            return CWLB_OK;
+        }
         for (size_t off = 0; off < bytes; off += kStageBytes) {
             const size_t n = std::min(kStageBytes, bytes - off);
             const unsigned b = next++ & 1u;
@@ -160,6 +179,12 @@ struct Stager {
 
     cwlb_status to_host(void* h_dst, const void* d_src, size_t bytes)
     {
+        if (direct) {
+            if (bytes)
+                CWLB_HIP_TRY(hipMemcpyAsync(h_dst, d_src, bytes, hipMemcpyDeviceToHost,
+                                            ctx->stream));
+            return CWLB_OK;
+        }
         size_t prev_off = 0, prev_n = 0;
         unsigned prev_b = 0;
         bool pending = false;
@@ -479,8 +504,7 @@ cwlb_status cwlb_spmm_mean_f32_host(cwlb_ctx* ctx, const int32_t* row_ptr,
         if (bad) bad_ci = true;
     });
     if (bad_ci) return fail(CWLB_INVALID_ARG, "spmm: column index outside [0, h_rows)");
-    cwlb_status s = ensure_staging(ctx);
-    if (s != CWLB_OK) return s;
+    const bool staged = ensure_staging(ctx);
     DevBuf<int32_t> d_rp, d_ci, d_or;
     DevBuf<float> d_val, d_H, d_C;
     DevBuf<cwlb_task> d_t;
@@ -492,8 +516,8 @@ cwlb_status cwlb_spmm_mean_f32_host(cwlb_ctx* ctx, const int32_t* row_ptr,
     CWLB_HIP_TRY(d_C.alloc(out_elems));
     CWLB_HIP_TRY(d_t.alloc(static_cast<size_t>(n_tasks)));
     hipStream_t st = ctx->stream;
-    Stager io{ctx};
-    s = io.to_device(d_rp.p, row_ptr, sizeof(int32_t) * (n_rows + 1));
+    Stager io{ctx, !staged};
+    cwlb_status s = io.to_device(d_rp.p, row_ptr, sizeof(int32_t) * (n_rows + 1));
     if (s == CWLB_OK) s = io.to_device(d_ci.p, col_idx, sizeof(int32_t) * nnz);
     if (s == CWLB_OK) s = io.to_device(d_val.p, val, sizeof(float) * nnz);
     if (s == CWLB_OK) s = io.to_device(d_or.p, origin, sizeof(int32_t) * n_rows);

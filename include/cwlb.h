@@ -206,7 +206,8 @@ cwlb_status cwlb_ctx_tune_schedule(cwlb_ctx* ctx, const int32_t* row_ptr, const 
  * The host arrays may be pageable: transfers go through two 64 MiB pinned
  * staging buffers that the context allocates at its first host-pointer call
  * and keeps until cwlb_ctx_destroy, filled and drained by up to 8 host
- * threads while the DMA engine moves the other buffer. */
+ * threads while the DMA engine moves the other buffer (if pinned memory is
+ * refused, the arrays are copied directly). */
 cwlb_status cwlb_spmm_mean_f32_host(cwlb_ctx* ctx, const int32_t* row_ptr,
                                     const int32_t* col_idx, const float* val,
                                     const int32_t* origin, int32_t n_rows, int64_t nnz,
