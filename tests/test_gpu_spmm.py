@@ -530,6 +530,32 @@ def test_host_pointer_entry_multi_chunk(gpu_ctx):
     check(got2, oracle.spmm_mean_f32(p2.row_ptr, p2.col_idx, p2.val, p2.origin, H2, p2.tasks))
 
 
+@pytest.mark.parametrize("K", [64, 128, 600])
+@pytest.mark.parametrize("h_off,c_off", [(1, 0), (2, 2), (0, 1), (3, 2)])
+def test_misaligned_feature_and_output_pointers(gpu_ctx, K, h_off, c_off):
+    """H and C handed over as views that start 4 or 8 bytes past a 16-byte
+    boundary: the kernel falls back to 8- or 4-byte lanes and still matches
+    the oracle; the floats around the output view are left untouched."""
+    torch = torch_mod()
+    g = workloads.small(4, seed=21)
+    H = synth.features(g.n, K, 4)
+    p = problem(g, SKEWED_COSTS, 24)
+    d_rp, d_ci, d_v, d_o = dev(p.row_ptr), dev(p.col_idx), dev(p.val), dev(p.origin)
+    d_t = dev(np.ascontiguousarray(p.tasks, np.int32).reshape(-1))
+    h_buf = torch.zeros(g.n * K + 8, dtype=torch.float32, device="cuda")
+    h_buf[h_off:h_off + g.n * K] = torch.from_numpy(H.reshape(-1)).cuda()
+    d_H = h_buf[h_off:h_off + g.n * K].view(g.n, K)
+    c_buf = torch.full((g.n * K + 8,), -5.0, dtype=torch.float32, device="cuda")
+    d_C = c_buf[c_off:c_off + g.n * K].view(g.n, K)
+    gpu_ctx.spmm(d_rp, d_ci, d_v, d_o, g.n, g.nnz, d_H, g.n, K, d_t, len(p.tasks), d_C)
+    ref32, ref64 = oracle_pair(p, g, H)
+    got = d_C.cpu().numpy()
+    check(got, ref32)
+    check(got, ref64)
+    rest = torch.cat([c_buf[:c_off], c_buf[c_off + g.n * K:]]).cpu().numpy()
+    assert np.all(rest == -5.0)
+
+
 def test_repeat_runs_stable(gpu_ctx):
     """Full rows are written identically on every run; split rows within tolerance."""
     g = workloads.small(4, seed=4)
