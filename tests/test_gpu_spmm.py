@@ -556,6 +556,30 @@ def test_misaligned_feature_and_output_pointers(gpu_ctx, K, h_off, c_off):
     assert np.all(rest == -5.0)
 
 
+@pytest.mark.parametrize("K", [32, 128])
+def test_nan_and_inf_features_propagate(gpu_ctx, K):
+    """Non-finite features propagate as in the reference's fma sums: a row
+    that gathers a NaN (or both infinities) gives NaN, one that gathers
+    +Inf only gives +Inf, and rows that gather neither stay finite and
+    match the oracle."""
+    g = workloads.small(4, seed=17)
+    H = synth.features(g.n, K, 8)
+    rng = np.random.default_rng(K)
+    H[rng.choice(g.n, 20, replace=False), rng.integers(0, K, 20)] = np.nan
+    H[rng.choice(g.n, 20, replace=False), rng.integers(0, K, 20)] = np.inf
+    H[rng.choice(g.n, 20, replace=False), rng.integers(0, K, 20)] = -np.inf
+    for S in (4, 1000):
+        p = problem(g, UNIT_COSTS, S)
+        got, _ = run_gpu(gpu_ctx, p, H)
+        ref32 = oracle.spmm_mean_f32(p.row_ptr, p.col_idx, p.val, p.origin, H, p.tasks)
+        assert np.array_equal(np.isnan(got), np.isnan(ref32))
+        assert np.array_equal(np.isposinf(got), np.isposinf(ref32))
+        assert np.array_equal(np.isneginf(got), np.isneginf(ref32))
+        fin = np.isfinite(ref32)
+        np.testing.assert_allclose(got[fin], ref32[fin], rtol=RTOL, atol=ATOL)
+        assert np.isnan(got).any() and np.isposinf(got).any()
+
+
 def test_repeat_runs_stable(gpu_ctx):
     """Full rows are written identically on every run; split rows within tolerance."""
     g = workloads.small(4, seed=4)
