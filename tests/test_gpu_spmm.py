@@ -580,6 +580,64 @@ def test_nan_and_inf_features_propagate(gpu_ctx, K):
         assert np.isnan(got).any() and np.isposinf(got).any()
 
 
+def test_two_contexts_on_two_threads(gpu_ctx):
+    """Two contexts, each on its own (default-priority) stream and host
+    thread, run different problems at the same time, one of them with runs
+    sorted by output row and the host-pointer entry in between: each gets
+    its own result, and an error on one thread does not leak into the other
+    thread's last-error message."""
+    import threading
+    torch = torch_mod()
+    probs = []
+    for cfg, K, seed in ((4, 128, 31), (5, 32, 32)):
+        g = workloads.small(cfg, seed=seed)
+        H = synth.features(g.n, K, seed)
+        p = problem(g, SKEWED_COSTS, 16)
+        probs.append((g, H, p, K, oracle.spmm_mean_f32(p.row_ptr, p.col_idx, p.val, p.origin,
+                                                         H, p.tasks)))
+    errors, results = [], [None, None]
+
+    def worker(i):
+        try:
+            g, H, p, K, ref = probs[i]
+            stream = torch.cuda.Stream()
+            ctx = capi.Context(0, stream.cuda_stream)
+            if i == 1:
+                ctx.set_locality(2, 2)
+            with torch.cuda.stream(stream):
+                d_rp, d_ci, d_v, d_o = dev(p.row_ptr), dev(p.col_idx), dev(p.val), dev(p.origin)
+                d_t = dev(np.ascontiguousarray(p.tasks, np.int32).reshape(-1))
+                d_H = dev(H)
+                C = torch.full((g.n, K), float("nan"), dtype=torch.float32, device="cuda")
+            stream.synchronize()
+            for it in range(20):
+                ctx.spmm(d_rp, d_ci, d_v, d_o, g.n, g.nnz, d_H, g.n, K, d_t, len(p.tasks), C)
+                if it == 10:
+                    got_h, _ = ctx.spmm_host(p.row_ptr, p.col_idx, p.val, p.origin, H, p.tasks)
+                    np.testing.assert_allclose(got_h, ref, rtol=RTOL, atol=ATOL)
+                if i == 0 and it == 5:
+                    with pytest.raises(capi.CwlbError):
+                        ctx.set_schedule(-1, 0)
+            stream.synchronize()
+            results[i] = C.cpu().numpy()
+            ctx.close()
+        except Exception as e:  # reported by the main thread
+            errors.append((i, repr(e)))
+
+    with pytest.raises(capi.CwlbError):
+        gpu_ctx.set_locality(5, 0)  # this thread's last error: the run_order message
+    threads = [threading.Thread(target=worker, args=(i,)) for i in range(2)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=120)
+    assert not any(t.is_alive() for t in threads)
+    assert not errors, errors
+    for i in range(2):
+        check(results[i], probs[i][4])
+    assert b"run_order" in capi.lib().cwlb_last_error()
+
+
 def test_repeat_runs_stable(gpu_ctx):
     """Full rows are written identically on every run; split rows within tolerance."""
     g = workloads.small(4, seed=4)
