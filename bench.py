@@ -253,8 +253,7 @@ def main():
         log(f"fixed schedule: {schedule}")
     elif not args.no_tune:
         t0 = time.perf_counter()
-        m, sl, (order, xcd) = ctx.tune_schedule(d_rp, d_ci, d_v, d_o, g.n, g.nnz, H, g.n, K, d_t,
-                                                T, C, trials=3, locality=True)
+        m, sl, (order, xcd) = tune(d_t, T)
         schedule.update(tasks_per_wave=m, feature_slices=sl, run_order=order, xcd_blocks=xcd,
                         tuned=True, tuning_ms=round((time.perf_counter() - t0) * 1e3, 1))
         log(f"tuned schedule: {schedule}")
