@@ -118,3 +118,73 @@ def test_planted_partition_mistake_fails_fixture(m):
     finally:
         oracle.set_mutation(0)
     assert wrong > 0
+
+
+# ------------------------------------------- S selection and the cost file
+HOST = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "host_golden.json")))
+
+
+def test_candidate_w_and_capacity_match_reference_fixture():
+    for c in HOST["recommended_candidate_w"]:
+        assert oracle.recommended_candidate_w(c["nnz"]) == c["w"], c
+        assert capi.recommended_candidate_w(c["nnz"]) == c["w"], c
+    for c in HOST["capacity_from_s"]:
+        cap = float.fromhex(c["capacity"])
+        assert oracle.capacity_from_s(c["s"], c["costs"]) == cap, c
+        assert capi.capacity_from_s(c["s"], c["costs"]) == cap, c
+
+
+def test_wave_based_s_matches_reference_fixture():
+    for c in HOST["wave_based_s"]:
+        if c["error"] is None:
+            assert oracle.wave_based_s(c["nnz"], 2, c["cu"], c["wave"]) == c["s"], c
+            assert capi.wave_based_s(c["nnz"], 2, c["cu"], c["wave"]) == c["s"], c
+        else:
+            assert oracle.wave_based_s(c["nnz"], 2, c["cu"], c["wave"]) == -1, c
+            with pytest.raises(capi.CwlbError) as e:
+                capi.wave_based_s(c["nnz"], 2, c["cu"], c["wave"])
+            assert e.value.status == capi.INVALID_ARG
+
+
+def test_candidate_search_matches_reference_fixture():
+    for c in HOST["candidate_search_bounds"]:
+        if c["error"] is None:
+            assert list(oracle.candidate_search_bounds(c["values"], c["best"])) == c["bounds"]
+            assert list(capi.candidate_search_bounds(c["values"], c["best"])) == c["bounds"]
+        else:
+            with pytest.raises(ValueError):
+                oracle.candidate_search_bounds(c["values"], c["best"])
+            with pytest.raises(capi.CwlbError):
+                capi.candidate_search_bounds(c["values"], c["best"])
+    for name in ("candidate_search_by_count", "candidate_search_by_step"):
+        for c in HOST[name]:
+            args = (c["lower"], c["upper"], c["third"])
+            if c["error"] is None:
+                assert getattr(oracle, name)(*args) == c["values"], (name, c)
+                assert getattr(capi, name)(*args) == c["values"], (name, c)
+            else:
+                with pytest.raises(ValueError):
+                    getattr(oracle, name)(*args)
+                with pytest.raises(capi.CwlbError):
+                    getattr(capi, name)(*args)
+
+
+def test_positive_search_argument_matches_reference_fixture():
+    from dropin_util import ProbeError, probe
+    for c in HOST["positive_search_argument"]:
+        if c["error"] is None:
+            assert probe("posarg", c["text"]).split()[1] == str(c["value"]), c
+        else:
+            with pytest.raises(ProbeError) as e:
+                probe("posarg", c["text"])
+            assert (e.value.kind == "invalid_argument") == (c["error"] == "invalid_argument"), c
+
+
+def test_cost_files_match_reference_fixture(tmp_path):
+    for c in HOST["cost_files"]:
+        assert oracle.format_costs(c["costs"], c["precision"]) == c["text"], c
+        path = tmp_path / "costs.txt"
+        capi.save_costs(c["costs"], path, precision=c["precision"])
+        assert path.read_text() == c["text"], c
+        if c["precision"] == 6:
+            assert list(capi.read_costs(path)) == [float(f"{x:.6f}") for x in c["costs"]]
