@@ -88,6 +88,7 @@ def segment_size_sweep(ctx, call, tune, dev, tasks_for, cfg, costs, S, trials):
     d_t = dev(tk.reshape(-1))
     ctx.set_schedule(0, 0)
     ctx.set_locality(0, 0)
+    ctx.set_cache_hints(0)
     for _ in range(3):
         call(d_t, len(tk), False)
     auto_us = float(np.mean([call(d_t, len(tk), True).main_us for _ in range(trials)]))
@@ -98,7 +99,7 @@ def segment_size_sweep(ctx, call, tune, dev, tasks_for, cfg, costs, S, trials):
     return {"S": S, "tasks": int(len(tk)), "automatic_us": round(auto_us, 1),
             "tuned_us": round(tuned_us, 1),
             "schedule": {"tasks_per_wave": m, "feature_slices": sl, "run_order": order,
-                         "xcd_blocks": xcd},
+                         "xcd_blocks": xcd, "hot_bytes": ctx.cache_hints()},
             "tasks_match_reference_fixture": reference_partition_match(cfg, S, costs, tk)}
 
 
@@ -169,6 +170,9 @@ def main():
                     help="comma-separated segment sizes timed after the measured step, each "
                          "with the automatic and the tuned schedule (default: 32,64,128,256,512 "
                          "for the mesh workload, none otherwise; 'none' for none)")
+    ap.add_argument("--hot-mb", type=int, default=0,
+                    help="fixed cache hints: hot set of this many MB of feature rows "
+                         "(cwlb_ctx_set_cache_hints; with --tasks-per-wave etc.)")
     ap.add_argument("--no-tune", action="store_true",
                     help="keep the automatic launch schedule (no cwlb_ctx_tune_schedule)")
     ap.add_argument("--no-host-call", action="store_true",
@@ -245,17 +249,20 @@ def main():
     # (cwlb_ctx_tune_schedule; 0, 0 = the automatic choice won).
     schedule = {"tasks_per_wave": 0, "feature_slices": 0, "tuned": False,
                 "automatic_schedule_us": round(float(auto_us), 1)}
-    if args.tasks_per_wave or args.slices or args.run_order or args.xcd_blocks:
+    if args.tasks_per_wave or args.slices or args.run_order or args.xcd_blocks or args.hot_mb:
         ctx.set_schedule(args.tasks_per_wave, args.slices)
         ctx.set_locality(args.run_order, args.xcd_blocks)
+        ctx.set_cache_hints(args.hot_mb << 20)
         schedule.update(tasks_per_wave=args.tasks_per_wave, feature_slices=args.slices,
-                        run_order=args.run_order, xcd_blocks=args.xcd_blocks)
+                        run_order=args.run_order, xcd_blocks=args.xcd_blocks,
+                        hot_bytes=args.hot_mb << 20)
         log(f"fixed schedule: {schedule}")
     elif not args.no_tune:
         t0 = time.perf_counter()
         m, sl, (order, xcd) = tune(d_t, T)
         schedule.update(tasks_per_wave=m, feature_slices=sl, run_order=order, xcd_blocks=xcd,
-                        tuned=True, tuning_ms=round((time.perf_counter() - t0) * 1e3, 1))
+                        hot_bytes=ctx.cache_hints(), tuned=True,
+                        tuning_ms=round((time.perf_counter() - t0) * 1e3, 1))
         log(f"tuned schedule: {schedule}")
 
     # Timed region: W warm-ups, K steps, synchronised on both sides.
@@ -309,6 +316,7 @@ def main():
         log(f"S sweep: {s_sweep}")
         ctx.set_schedule(0, 0)
         ctx.set_locality(0, 0)
+        ctx.set_cache_hints(0)
 
     flops = 2.0 * g.nnz * K
     gflops = flops / (ms_per_step * 1e-3) / 1e9

@@ -45,6 +45,21 @@ struct cwlb_ctx {
     int order_M = 0;
     void* d_sort_temp = nullptr;
     size_t sort_temp_bytes = 0;
+    // Cache-policy hints of the feature-row gathers (0 = off): the hot set
+    // in bytes of feature rows, the per-column in-degrees, their histogram
+    // and the per-nonzero cold bits, with what they were built for.
+    long long sched_hot_bytes = 0;
+    unsigned* d_col_counts = nullptr;
+    long long col_count_cap = 0;
+    unsigned* d_count_hist = nullptr;
+    unsigned long long* d_hints = nullptr;
+    long long hint_cap = 0;
+    const void* hint_col = nullptr;
+    long long hint_nnz = -1;
+    long long hint_h_rows = -1;
+    long long hint_hot_rows = -1;
+    unsigned hint_theta = 0;
+    bool hint_any_cold = false;
     // Pinned host staging of the host-pointer entry point: two buffers used
     // alternately, each with the event of the last transfer through it.
     void* h_stage[2] = {nullptr, nullptr};
@@ -120,6 +135,12 @@ cwlb_status launch_partition(cwlb_ctx* ctx, const int32_t* row_ptr, int32_t n_ro
                              cwlb_task* out, int64_t capacity_tasks, int64_t* n_tasks);
 
 cwlb_status launch_fill_features(cwlb_ctx* ctx, float* H, int64_t rows, int32_t K, uint64_t seed);
+
+// Builds (or reuses) the per-nonzero cold-column bits for a hot set of
+// hot_rows feature rows (csrc/col_hints.hip); synchronises when it builds.
+// *hints is null when no column is cold.
+cwlb_status build_cache_hints(cwlb_ctx* ctx, const SpmmArgs& a, long long hot_rows,
+                              const unsigned long long** hints);
 
 cwlb_status launch_reorder(cwlb_ctx* ctx, int32_t n_rows, int64_t nnz, const int32_t* row_ptr,
                            const int32_t* col_idx, const float* val, int32_t* origin,

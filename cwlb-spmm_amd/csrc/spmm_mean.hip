@@ -92,6 +92,36 @@ __device__ __forceinline__ void vstore_nt(float* p, typename VecT<VEC>::T v)
     __builtin_nontemporal_store(v, reinterpret_cast<typename VecT<VEC>::T*>(p));
 }
 
+// Feature-row gathers under cache-policy hints: a raw buffer resource over
+// H (byte offsets below 4 GiB, bounds-checked by the hardware), and one
+// 16-byte load whose policy is non-temporal for a cold column.  The policy
+// is an immediate of the load instruction, so the two loads stay distinct.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t feature_rsrc(const float* H, long long h_rows,
+                                                               int ld)
+{
+    const unsigned long long bytes = static_cast<unsigned long long>(h_rows) * ld * 4ull;
+    return __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(H), 0,
+        bytes > 0xFFFFFFFFull ? 0xFFFFFFFFu : static_cast<unsigned>(bytes), 0x00020000);
+}
+
+__device__ __forceinline__ f4 gather_hinted(__amdgpu_buffer_rsrc_t r, unsigned byte_off, bool cold)
+{
+    if (cold) return __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 2));
+    return __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0));
+}
+
+// Bit 31 of a staged column index carries the cold hint of its nonzero
+// (valid column indices are below 2^31; a negative, invalid one becomes
+// INT_MAX, which the column bounds check still rejects).
+__device__ __forceinline__ int with_hint(int col, const unsigned long long* __restrict__ hints,
+                                         long long j)
+{
+    const unsigned cold = static_cast<unsigned>((hints[j >> 6] >> (j & 63)) & 1ull);
+    const unsigned c = col < 0 ? 0x7fffffffu : static_cast<unsigned>(col);
+    return static_cast<int>(c | (cold << 31));
+}
+
 __device__ __forceinline__ float vfma(float a, float h, float c) { return __builtin_fmaf(a, h, c); }
 __device__ __forceinline__ f2 vfma(float a, f2 h, f2 c)
 {
@@ -254,15 +284,17 @@ __device__ __forceinline__ void block_slice(int& slice, long long& jb, long long
                    : static_cast<long long>(bx >> 3) * P + q;
 }
 
-template <int VEC, int G, int R, int U, int SL>
+template <int VEC, int G, int R, int U, int SL, bool HN>
 __global__ void __launch_bounds__(kBlock)
 spmm_mean_runs(const int* __restrict__ rp, const int* __restrict__ ci,
                const float* __restrict__ val, const int* __restrict__ origin, int n_rows,
                long long nnz, const float* __restrict__ H, long long h_rows, int ld,
                const cwlb_task* __restrict__ tasks, long long n_tasks, int M, long long n_runs,
                long long n_blocks, long long chunk, const int* __restrict__ run_order,
-               float* __restrict__ C, int* __restrict__ status)
+               const unsigned long long* __restrict__ hints, float* __restrict__ C,
+               int* __restrict__ status)
 {
+    static_assert(!HN || VEC == 4, "hinted gathers move 16 bytes per lane");
     using V = typename VecT<VEC>::T;
     constexpr int NS = 64 / G;                     // row slots per wave
     constexpr int RU = cmin(cmin(U, 4), G);        // rows per slot (short rows)
@@ -310,6 +342,10 @@ spmm_mean_runs(const int* __restrict__ rp, const int* __restrict__ ci,
     const int F = K / VEC;
     const int npass = (F + G * R - 1) / (G * R);
     int bad = 0;
+    // Hinted gathers: byte offset of feature vector f of column c's slice.
+    __amdgpu_buffer_rsrc_t hrsrc;
+    if constexpr (HN) hrsrc = feature_rsrc(H, h_rows, ld);
+    const unsigned slice_bytes = static_cast<unsigned>(slice * K) * 4u;
 
     for (int pass = 0; pass < npass; ++pass) {
         const int fl = pass * G * R + sub;  // first vector element of this lane
@@ -330,17 +366,21 @@ spmm_mean_runs(const int* __restrict__ rp, const int* __restrict__ ci,
                     if (lane < wn) {
                         colw = __builtin_nontemporal_load(ci + c0.base + w0 + lane);
                         valw = __builtin_nontemporal_load(val + c0.base + w0 + lane);
+                        if constexpr (HN) colw = with_hint(colw, hints, c0.base + w0 + lane);
                     }
                     for (int k0 = 0; k0 < wn; k0 += STEP) {
                         int cc[UL];
                         float a[UL];
                         bool ok[UL];
+                        bool cold[UL];
                         const int sl = fresh(slot);
 #pragma unroll
                         for (int u = 0; u < UL; ++u) {
                             const int jj = k0 + u * NS + sl;
                             cc[u] = __shfl(colw, jj & 63);
                             a[u] = __shfl(valw, jj & 63);
+                            cold[u] = HN && cc[u] < 0;
+                            if constexpr (HN) cc[u] &= 0x7fffffff;
                             ok[u] = jj < wn;
                             if (ok[u] && static_cast<unsigned long long>(cc[u]) >=
                                              static_cast<unsigned long long>(h_rows)) {
@@ -355,8 +395,16 @@ spmm_mean_runs(const int* __restrict__ rp, const int* __restrict__ ci,
 #pragma unroll
                             for (int q = 0; q < R; ++q) {
                                 const int f = fl + G * q;
-                                h[u][q] = (ok[u] && f < F) ? vload<VEC>(hrow + f * VEC)
-                                                           : vzero<VEC>();
+                                if constexpr (HN)
+                                    h[u][q] = (ok[u] && f < F)
+                                                  ? gather_hinted(hrsrc,
+                                                                  static_cast<unsigned>(cc[u]) * ld * 4u +
+                                                                      slice_bytes + f * 16u,
+                                                                  cold[u])
+                                                  : vzero<VEC>();
+                                else
+                                    h[u][q] = (ok[u] && f < F) ? vload<VEC>(hrow + f * VEC)
+                                                               : vzero<VEC>();
                             }
                         }
 #pragma unroll
@@ -439,6 +487,8 @@ spmm_mean_runs(const int* __restrict__ rp, const int* __restrict__ ci,
                     const int i = lane + 64 * t;
                     lc[t] = i < gn ? __builtin_nontemporal_load(ci + gs + i) : 0;
                     lv[t] = i < gn ? __builtin_nontemporal_load(val + gs + i) : 0.0f;
+                    if constexpr (HN)
+                        if (i < gn) lc[t] = with_hint(lc[t], hints, gs + i);
                 }
 #pragma unroll
                 for (int t = 0; t < NT; ++t) {
@@ -454,6 +504,7 @@ spmm_mean_runs(const int* __restrict__ rp, const int* __restrict__ ci,
             } else if (lane < gn) {
                 colw = __builtin_nontemporal_load(ci + gs + lane);
                 valw = __builtin_nontemporal_load(val + gs + lane);
+                if constexpr (HN) colw = with_hint(colw, hints, gs + lane);
             }
             V acc[RU][R];
             int pos[RU];
@@ -474,6 +525,7 @@ spmm_mean_runs(const int* __restrict__ rp, const int* __restrict__ ci,
                 int cc[RU];
                 float a[RU];
                 bool ok[RU];
+                bool cold[RU];
 #pragma unroll
                 for (int u = 0; u < RU; ++u) {
                     ok[u] = j < len[u];
@@ -485,6 +537,8 @@ spmm_mean_runs(const int* __restrict__ rp, const int* __restrict__ ci,
                         cc[u] = __shfl(colw, src & 63);
                         a[u] = __shfl(valw, src & 63);
                     }
+                    cold[u] = HN && cc[u] < 0;
+                    if constexpr (HN) cc[u] &= 0x7fffffff;
                     if (ok[u] && static_cast<unsigned long long>(cc[u]) >=
                                      static_cast<unsigned long long>(h_rows)) {
                         ok[u] = false;
@@ -498,7 +552,15 @@ spmm_mean_runs(const int* __restrict__ rp, const int* __restrict__ ci,
 #pragma unroll
                     for (int q = 0; q < R; ++q) {
                         const int f = fl + G * q;
-                        h[u][q] = (ok[u] && f < F) ? vload<VEC>(hrow + f * VEC) : vzero<VEC>();
+                        if constexpr (HN)
+                            h[u][q] = (ok[u] && f < F)
+                                          ? gather_hinted(hrsrc,
+                                                          static_cast<unsigned>(cc[u]) * ld * 4u +
+                                                              slice_bytes + f * 16u,
+                                                          cold[u])
+                                          : vzero<VEC>();
+                        else
+                            h[u][q] = (ok[u] && f < F) ? vload<VEC>(hrow + f * VEC) : vzero<VEC>();
                     }
                 }
 #pragma unroll
@@ -655,17 +717,34 @@ struct Plan {
     long long grid;        // launched blocks
     bool ordered;          // runs execute sorted by output row id
     const int* order;      // that order (device), set at launch
+    const unsigned long long* hints;  // cold-column bits (device) or null
 };
 
-template <int VEC, int G, int R, int SL>
+template <int VEC, int G, int R, int SL, bool HN = false>
 void launch_main(hipStream_t st, const SpmmArgs& a, const Plan& p, int* status)
 {
     constexpr int U = (R == 1) ? 8 : (R == 2) ? 4 : (R <= 4) ? 2 : 1;
-    hipLaunchKernelGGL((spmm_mean_runs<VEC, G, R, U, SL>), dim3(static_cast<unsigned>(p.grid)),
-                       dim3(kBlock), 0, st, a.row_ptr, a.col_idx, a.val, a.origin, a.n_rows,
-                       static_cast<long long>(a.nnz), a.H, static_cast<long long>(a.h_rows), a.K,
-                       a.tasks, static_cast<long long>(a.n_tasks), p.M, p.runs, p.blocks, p.chunk,
-                       p.order, a.C, status);
+    hipLaunchKernelGGL((spmm_mean_runs<VEC, G, R, U, SL, HN>),
+                       dim3(static_cast<unsigned>(p.grid)), dim3(kBlock), 0, st, a.row_ptr,
+                       a.col_idx, a.val, a.origin, a.n_rows, static_cast<long long>(a.nnz), a.H,
+                       static_cast<long long>(a.h_rows), a.K, a.tasks,
+                       static_cast<long long>(a.n_tasks), p.M, p.runs, p.blocks, p.chunk, p.order,
+                       p.hints, a.C, status);
+}
+
+// Feature slices of one lane group (one vector per lane) under cache hints.
+template <int VEC, int SL>
+void dispatch_hinted(hipStream_t st, const SpmmArgs& a, const Plan& p, int* status, int G)
+{
+    switch (G) {
+    case 1: return launch_main<VEC, 1, 1, SL, true>(st, a, p, status);
+    case 2: return launch_main<VEC, 2, 1, SL, true>(st, a, p, status);
+    case 4: return launch_main<VEC, 4, 1, SL, true>(st, a, p, status);
+    case 8: return launch_main<VEC, 8, 1, SL, true>(st, a, p, status);
+    case 16: return launch_main<VEC, 16, 1, SL, true>(st, a, p, status);
+    case 32: return launch_main<VEC, 32, 1, SL, true>(st, a, p, status);
+    default: return launch_main<VEC, 64, 1, SL, true>(st, a, p, status);
+    }
 }
 
 template <int VEC, int SL>
@@ -675,6 +754,9 @@ void dispatch_width(hipStream_t st, const SpmmArgs& a, const Plan& p, int* statu
     if (F <= 64) {
         int G = 1;
         while (G < F) G <<= 1;
+        if constexpr (VEC == 4) {
+            if (p.hints) return dispatch_hinted<VEC, SL>(st, a, p, status, G);
+        }
         switch (G) {
         case 1: return launch_main<VEC, 1, 1, SL>(st, a, p, status);
         case 2: return launch_main<VEC, 2, 1, SL>(st, a, p, status);
@@ -785,6 +867,7 @@ Plan make_plan(const cwlb_ctx* ctx, const SpmmArgs& a, bool per_task)
     }
     p.ordered = !per_task && ctx->sched_order == 2 && p.runs > 1;
     p.order = nullptr;
+    p.hints = nullptr;
     return p;
 }
 
@@ -800,6 +883,15 @@ cwlb_status launch_spmm_mean(cwlb_ctx* ctx, const SpmmArgs& a, bool zero_all, bo
         return fail(CWLB_UNSUPPORTED,
                     "spmm: too many runs for one launch (more than 2^32 work-items); use more "
                     "tasks per wave (cwlb_ctx_set_schedule) or a larger S");
+    // Cache hints: 16-byte lanes, one vector per lane and slice, and the
+    // feature matrix addressable by 32-bit byte offsets.
+    if (!per_task && ctx->sched_hot_bytes > 0 && p.vec == 4 && a.n_tasks > 0 && a.K > 0 &&
+        a.K / p.sl <= 256 &&
+        static_cast<unsigned long long>(a.h_rows) * a.K * 4ull <= 0xFFFFFFFFull) {
+        const long long hot_rows = ctx->sched_hot_bytes / (4ll * a.K);
+        const cwlb_status s = build_cache_hints(ctx, a, hot_rows, &p.hints);
+        if (s != CWLB_OK) return s;
+    }
     if (record_events) CWLB_HIP_TRY(hipEventRecord(ctx->ev[0], st));
     const long long total = static_cast<long long>(a.n_rows) * a.K;
     if (zero_all) {

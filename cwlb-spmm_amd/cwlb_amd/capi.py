@@ -23,7 +23,8 @@ PER_TASK = 0x2
 EXPORTS = [
     "cwlb_version", "cwlb_last_error", "cwlb_ctx_create", "cwlb_ctx_destroy",
     "cwlb_ctx_set_stream", "cwlb_ctx_synchronize", "cwlb_ctx_device_info", "cwlb_ctx_set_schedule",
-    "cwlb_ctx_set_locality", "cwlb_ctx_tune_schedule",
+    "cwlb_ctx_set_locality", "cwlb_ctx_set_cache_hints", "cwlb_ctx_get_cache_hints",
+    "cwlb_ctx_tune_schedule",
     "cwlb_spmm_mean_f32", "cwlb_spmm_mean_f32_large_k", "cwlb_spmm_mean_f32_host",
     "cwlb_reorder_by_degree", "cwlb_reorder_by_degree_device", "cwlb_partition",
     "cwlb_partition_device",
@@ -99,6 +100,8 @@ def lib():
         L.cwlb_ctx_device_info.argtypes = [vp, C.POINTER(DeviceInfo)]
         L.cwlb_ctx_set_schedule.argtypes = [vp, i32, i32]
         L.cwlb_ctx_set_locality.argtypes = [vp, i32, i32]
+        L.cwlb_ctx_set_cache_hints.argtypes = [vp, i64]
+        L.cwlb_ctx_get_cache_hints.argtypes = [vp, C.POINTER(i64)]
         L.cwlb_ctx_tune_schedule.argtypes = [vp, vp, vp, vp, vp, i32, i64, vp, i64, i32, vp, i64,
                                              vp, i32, C.POINTER(i32), C.POINTER(i32), vp]
         spmm = [vp, vp, vp, vp, vp, i32, i64, vp, i64, i32, vp, i64, vp, u32, C.POINTER(Timing)]
@@ -265,6 +268,14 @@ class Context:
 
     def set_locality(self, run_order=0, xcd_blocks=0):
         check(lib().cwlb_ctx_set_locality(self.h, int(run_order), int(xcd_blocks)))
+
+    def set_cache_hints(self, hot_bytes=0):
+        check(lib().cwlb_ctx_set_cache_hints(self.h, int(hot_bytes)))
+
+    def cache_hints(self):
+        v = i64()
+        check(lib().cwlb_ctx_get_cache_hints(self.h, C.byref(v)))
+        return v.value
 
     def tune_schedule(self, row_ptr, col_idx, val, origin, n_rows, nnz, H, h_rows, K, tasks,
                       n_tasks, C_out, trials=3, locality=False):

@@ -124,6 +124,24 @@ cwlb_status cwlb_ctx_set_schedule(cwlb_ctx* ctx, int32_t tasks_per_wave, int32_t
  * it. */
 cwlb_status cwlb_ctx_set_locality(cwlb_ctx* ctx, int32_t run_order, int32_t xcd_blocks);
 
+/* Cache-policy hints of later SpMM calls on this context.  hot_bytes = 0
+ * (the default): every feature row is loaded with the normal policy.
+ * hot_bytes > 0: the columns are ranked by in-degree; the feature rows of
+ * the most-gathered columns, about hot_bytes of them, keep the normal policy
+ * and the rest are loaded non-temporally, so that on skewed graphs the hot
+ * rows stay in L2 and the Infinity Cache.  The first call after a change of
+ * the column array, nnz, h_rows or hot_bytes builds one bit per nonzero in a
+ * context-owned device buffer (and synchronises the stream; that call cannot
+ * be captured into a HIP graph); later calls reuse it.  The hints steer
+ * only the cache policy: results are the same with or without them, and
+ * hints left over from earlier contents of col_idx only cost speed.
+ * Applies with 16-byte aligned H and C, K a multiple of 4, at most 256
+ * floats per feature slice and H below 4 GiB; otherwise ignored.  No
+ * counterpart in the reference; cwlb_ctx_tune_schedule tries 24, 48 and
+ * 96 MB. */
+cwlb_status cwlb_ctx_set_cache_hints(cwlb_ctx* ctx, int64_t hot_bytes);
+cwlb_status cwlb_ctx_get_cache_hints(cwlb_ctx* ctx, int64_t* hot_bytes);
+
 /* ------------------------------------------------------------ aggregation
  * C[Origin_local[r]][k] = (sum over the task chunks of row r of
  *   val[j] * H[col_idx[j]][k]) / deg(r)
@@ -188,8 +206,10 @@ cwlb_status cwlb_spmm_mean_f32_large_k(cwlb_ctx* ctx, const int32_t* row_ptr,
  * won).  With locality_out non-null (two int32), the fastest schedule is
  * also timed with runs sorted by output row (interleaved and contiguous XCD
  * placement, cwlb_ctx_set_locality), the winner is kept on the context and
- * written there (1, 0 or the context's previous setting = task order kept).
- * C receives the result.  Synchronises.  No counterpart in the reference,
+ * written there (1, 0 or the context's previous setting = task order kept);
+ * then with cache hints of 24, 48 and 96 MB (cwlb_ctx_set_cache_hints), the
+ * fastest kept on the context (0 = none; read it with
+ * cwlb_ctx_get_cache_hints).  C receives the result.  Synchronises.  No counterpart in the reference,
  * whose one task per work-group has nothing to tune; like its S search, it
  * is meant to run once per graph before timed runs. */
 cwlb_status cwlb_ctx_tune_schedule(cwlb_ctx* ctx, const int32_t* row_ptr, const int32_t* col_idx,

@@ -50,25 +50,30 @@ def run_gpu(ctx, p, H, flags=0, c_fill=float("nan"), large_k=False, h_dev=None):
     return C[:p.n, :K].cpu().numpy(), t
 
 
-# (tasks_per_wave, feature_slices, flags, run_order, xcd_blocks): automatic,
-# the reference's one task per wave, forced task-run fusion / XCD feature
-# slicing (small graphs do not trigger them automatically), runs sorted by
-# output row and contiguous XCD stretches.
-SCHEDULES = [(0, 0, 0, 0, 0), (0, 0, capi.PER_TASK, 0, 0), (3, 1, 0, 1, 1), (8, 2, 0, 1, 1),
-             (16, 4, 0, 1, 1), (64, 4, 0, 1, 1), (2, 1, 0, 2, 1), (5, 1, 0, 1, 2),
-             (8, 4, 0, 2, 2), (1, 2, 0, 2, 2)]
+# (tasks_per_wave, feature_slices, flags, run_order, xcd_blocks, hot_bytes):
+# automatic, the reference's one task per wave, forced task-run fusion / XCD
+# feature slicing (small graphs do not trigger them automatically), runs
+# sorted by output row, contiguous XCD stretches, and cache hints (hot sets
+# of 64 KB / 256 KB of feature rows: a few hundred hot columns, the rest
+# cold, on these small graphs).
+SCHEDULES = [(0, 0, 0, 0, 0, 0), (0, 0, capi.PER_TASK, 0, 0, 0), (3, 1, 0, 1, 1, 0),
+             (8, 2, 0, 1, 1, 0), (16, 4, 0, 1, 1, 0), (64, 4, 0, 1, 1, 0), (2, 1, 0, 2, 1, 0),
+             (5, 1, 0, 1, 2, 0), (8, 4, 0, 2, 2, 0), (1, 2, 0, 2, 2, 0), (0, 0, 0, 0, 0, 1 << 16),
+             (8, 2, 0, 1, 1, 1 << 18), (2, 1, 0, 2, 2, 1 << 16), (0, 0, capi.PER_TASK, 0, 0, 1 << 16)]
 SCHED_IDS = ["auto", "per_task", "m3", "m8s2", "m16s4", "m64s4", "m2ord", "m5xcd", "m8s4ordxcd",
-             "m1s2ordxcd"]
+             "m1s2ordxcd", "hints64k", "m8s2_hints256k", "m2ordxcd_hints64k", "per_task_hints"]
 
 
 @pytest.fixture(params=SCHEDULES, ids=SCHED_IDS)
 def sched(request, gpu_ctx):
-    m, sl, flags, order, xcd = request.param
+    m, sl, flags, order, xcd, hot = request.param
     gpu_ctx.set_schedule(m, sl)
     gpu_ctx.set_locality(order, xcd)
+    gpu_ctx.set_cache_hints(hot)
     yield flags
     gpu_ctx.set_schedule(0, 0)
     gpu_ctx.set_locality(0, 0)
+    gpu_ctx.set_cache_hints(0)
 
 
 def check(got, ref):
@@ -580,6 +585,107 @@ def test_nan_and_inf_features_propagate(gpu_ctx, K):
         assert np.isnan(got).any() and np.isposinf(got).any()
 
 
+@pytest.mark.parametrize("K", [32, 64, 128, 256])
+def test_cache_hints_change_no_value(gpu_ctx, K):
+    """Hot sets from a handful of columns to all of them: every result equals
+    the unhinted one (full rows bit for bit, split rows within tolerance) and
+    the oracle."""
+    torch = torch_mod()
+    g = workloads.small(4, seed=41)
+    H = synth.features(g.n, K, 12)
+    p = problem(g, SKEWED_COSTS, 16)
+    d_rp, d_ci, d_v, d_o = dev(p.row_ptr), dev(p.col_idx), dev(p.val), dev(p.origin)
+    d_t = dev(np.ascontiguousarray(p.tasks, np.int32).reshape(-1))
+    d_H = dev(H)
+    C0 = torch.full((g.n, K), float("nan"), dtype=torch.float32, device="cuda")
+    gpu_ctx.spmm(d_rp, d_ci, d_v, d_o, g.n, g.nnz, d_H, g.n, K, d_t, len(p.tasks), C0)
+    ref32 = oracle.spmm_mean_f32(p.row_ptr, p.col_idx, p.val, p.origin, H, p.tasks)
+    whole = np.ones(g.n, bool)
+    whole[p.origin[split_rows(p)]] = False
+    C1 = torch.full_like(C0, float("nan"))
+    try:
+        for hot in (4 * K, 64 * 4 * K, 1024 * 4 * K, g.n * 4 * K):
+            for m, sl in ((0, 0), (4, 2), (1, 1)):
+                gpu_ctx.set_schedule(m, sl)
+                gpu_ctx.set_cache_hints(hot)
+                C1.fill_(float("nan"))
+                gpu_ctx.spmm(d_rp, d_ci, d_v, d_o, g.n, g.nnz, d_H, g.n, K, d_t, len(p.tasks), C1)
+                got = C1.cpu().numpy()
+                check(got, ref32)
+                if (m, sl) == (0, 0):
+                    assert np.array_equal(got[whole], C0.cpu().numpy()[whole]), hot
+    finally:
+        gpu_ctx.set_schedule(0, 0)
+        gpu_ctx.set_cache_hints(0)
+
+
+def test_cache_hints_left_over_from_other_columns(gpu_ctx):
+    """Hints built for one column array stay in use after the caller rewrites
+    that array in place (same pointer and length): only the cache policy can
+    be off, the results follow the new columns.  A bad column index is still
+    reported with hints on."""
+    torch = torch_mod()
+    g = workloads.small(4, seed=43)
+    K = 64
+    H = synth.features(g.n, K, 13)
+    p = problem(g, UNIT_COSTS, 16)
+    d_rp, d_ci, d_v, d_o = dev(p.row_ptr), dev(p.col_idx), dev(p.val), dev(p.origin)
+    d_t = dev(np.ascontiguousarray(p.tasks, np.int32).reshape(-1))
+    d_H = dev(H)
+    C = torch.full((g.n, K), float("nan"), dtype=torch.float32, device="cuda")
+    gpu_ctx.set_cache_hints(64 * 4 * K)
+    try:
+        gpu_ctx.spmm(d_rp, d_ci, d_v, d_o, g.n, g.nnz, d_H, g.n, K, d_t, len(p.tasks), C)
+        check(C.cpu().numpy(), oracle.spmm_mean_f32(p.row_ptr, p.col_idx, p.val, p.origin, H,
+                                                    p.tasks))
+        perm = np.random.default_rng(3).permutation(g.n).astype(np.int32)
+        ci2 = perm[p.col_idx]
+        d_ci.copy_(torch.from_numpy(ci2).cuda())
+        C.fill_(float("nan"))
+        gpu_ctx.spmm(d_rp, d_ci, d_v, d_o, g.n, g.nnz, d_H, g.n, K, d_t, len(p.tasks), C)
+        check(C.cpu().numpy(), oracle.spmm_mean_f32(p.row_ptr, ci2, p.val, p.origin, H, p.tasks))
+        bad = ci2.copy()
+        bad[5] = -7
+        d_ci.copy_(torch.from_numpy(bad).cuda())
+        with pytest.raises(capi.CwlbError) as e:
+            gpu_ctx.spmm(d_rp, d_ci, d_v, d_o, g.n, g.nnz, d_H, g.n, K, d_t, len(p.tasks), C)
+        assert e.value.status == capi.INVALID_ARG
+    finally:
+        gpu_ctx.set_cache_hints(0)
+
+
+def test_cache_hints_ignored_beyond_4gib(gpu_ctx):
+    """A feature matrix of 4.3 GB (32-bit offsets do not reach its end): the
+    hints are not used and the result is still correct."""
+    torch = torch_mod()
+    g = workloads.small(4, seed=44)
+    K = 128
+    h_rows = (1 << 32) // (4 * K) + 4096
+    p = problem(g, UNIT_COSTS, 16)
+    d_H = torch.empty((h_rows, K), dtype=torch.float32, device="cuda")
+    gpu_ctx.fill_features(d_H, h_rows, K, 9)
+    ci = (p.col_idx.astype(np.int64) * (h_rows // g.n)).astype(np.int32)
+    H_used = d_H[torch.from_numpy(np.arange(g.n) * (h_rows // g.n)).cuda()].cpu().numpy()
+    d_rp, d_ci, d_v, d_o = dev(p.row_ptr), dev(ci), dev(p.val), dev(p.origin)
+    d_t = dev(np.ascontiguousarray(p.tasks, np.int32).reshape(-1))
+    C = torch.full((g.n, K), float("nan"), dtype=torch.float32, device="cuda")
+    gpu_ctx.set_cache_hints(1 << 20)
+    try:
+        gpu_ctx.spmm(d_rp, d_ci, d_v, d_o, g.n, g.nnz, d_H, h_rows, K, d_t, len(p.tasks), C)
+    finally:
+        gpu_ctx.set_cache_hints(0)
+    check(C.cpu().numpy(), oracle.spmm_mean_f32(p.row_ptr, p.col_idx, p.val, p.origin, H_used,
+                                                p.tasks))
+
+
+def test_cache_hints_argument(gpu_ctx):
+    with pytest.raises(capi.CwlbError):
+        gpu_ctx.set_cache_hints(-1)
+    gpu_ctx.set_cache_hints(12345)
+    assert gpu_ctx.cache_hints() == 12345
+    gpu_ctx.set_cache_hints(0)
+
+
 def test_two_contexts_on_two_threads(gpu_ctx):
     """Two contexts, each on its own (default-priority) stream and host
     thread, run different problems at the same time, one of them with runs
@@ -689,18 +795,21 @@ def test_full_config_locality_modes_agree(gpu_ctx, cfg):
     gpu_ctx.spmm(d_rp, d_ci, d_v, d_o, g.n, g.nnz, H, g.n, K, d_t, len(p.tasks), C0)
     C1 = torch.full_like(C0, float("nan"))
     try:
-        for m, order, xcd in ((4, 2, 1), (8, 2, 2), (32, 1, 2)):
+        for m, order, xcd, hot in ((4, 2, 1, 0), (8, 2, 2, 0), (32, 1, 2, 0), (64, 1, 1, 48 << 20),
+                                   (8, 2, 2, 96 << 20)):
             gpu_ctx.set_schedule(m, 0)
             gpu_ctx.set_locality(order, xcd)
+            gpu_ctx.set_cache_hints(hot)
             C1.fill_(float("nan"))
             gpu_ctx.spmm(d_rp, d_ci, d_v, d_o, g.n, g.nnz, H, g.n, K, d_t, len(p.tasks), C1)
             diff = (C1 - C0).abs()
             bound = RTOL * C0.abs() + ATOL
             assert not torch.isnan(C1).any().item()
-            assert bool((diff <= bound).all().item()), (m, order, xcd, diff.max().item())
+            assert bool((diff <= bound).all().item()), (m, order, xcd, hot, diff.max().item())
     finally:
         gpu_ctx.set_schedule(0, 0)
         gpu_ctx.set_locality(0, 0)
+        gpu_ctx.set_cache_hints(0)
 
 
 def test_async_call_reports_bad_column_at_synchronize(gpu_ctx):
@@ -776,6 +885,7 @@ def test_tune_schedule(gpu_ctx):
                                            len(p.tasks), C, trials=2, locality=True)
         assert (m, sl) == (0, 0) or (m in (2, 4, 8, 16, 32, 64) and sl in (1, 2, 4))
         assert loc in ((0, 0), (2, 1), (2, 2))
+        assert gpu_ctx.cache_hints() in (0, 24 << 20, 48 << 20, 96 << 20)
         ref32, ref64 = oracle_pair(p, g, H)
         check(C.cpu().numpy(), ref32)
         C.fill_(float("nan"))
@@ -789,6 +899,7 @@ def test_tune_schedule(gpu_ctx):
     finally:
         gpu_ctx.set_schedule(0, 0)
         gpu_ctx.set_locality(0, 0)
+        gpu_ctx.set_cache_hints(0)
 
 
 def test_run_order_reused_across_task_lists(gpu_ctx):
