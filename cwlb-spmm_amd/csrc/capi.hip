@@ -480,6 +480,9 @@ cwlb_status cwlb_ctx_tune_schedule(cwlb_ctx* ctx, const int32_t* row_ptr, const 
             if (st != CWLB_OK) break;
             ctx->sched_hot_bytes = mb << 20;
             st = run_spmm(ctx, a, 0, nullptr);  // warm-up, builds the hints
+            // Hints that do not apply to this call (K, alignment, H size) or
+            // mark no column cold leave nothing to time.
+            if (st != CWLB_OK || !ctx->last_call_hinted) break;
             for (int t = 0; st == CWLB_OK && t < trials; ++t) {
                 cwlb_timing tm{};
                 st = run_spmm(ctx, a, 0, &tm);

@@ -60,6 +60,7 @@ struct cwlb_ctx {
     long long hint_hot_rows = -1;
     unsigned hint_theta = 0;
     bool hint_any_cold = false;
+    bool last_call_hinted = false;  // the last aggregation launch used hints
     // Pinned host staging of the host-pointer entry point: two buffers used
     // alternately, each with the event of the last transfer through it.
     void* h_stage[2] = {nullptr, nullptr};

@@ -892,6 +892,7 @@ cwlb_status launch_spmm_mean(cwlb_ctx* ctx, const SpmmArgs& a, bool zero_all, bo
         const cwlb_status s = build_cache_hints(ctx, a, hot_rows, &p.hints);
         if (s != CWLB_OK) return s;
     }
+    ctx->last_call_hinted = p.hints != nullptr;
     if (record_events) CWLB_HIP_TRY(hipEventRecord(ctx->ev[0], st));
     const long long total = static_cast<long long>(a.n_rows) * a.K;
     if (zero_all) {
