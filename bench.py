@@ -280,6 +280,8 @@ def main():
     times = [call(d_t, T, True) for _ in range(args.steps)]
     main_us = float(np.mean([t.main_us for t in times]))
     zero_us = float(np.mean([t.zero_us for t in times]))
+    # The schedule those launches resolved to (automatic choices included).
+    schedule["launched"] = ctx.last_launch()
     # The reference's structure (one task per wave, one atomic add per
     # partial segment), for comparison.
     pt = [ctx.spmm(d_rp, d_ci, d_v, d_o, g.n, g.nnz, H, g.n, K, d_t, T, C,

@@ -367,6 +367,13 @@ cwlb_status cwlb_ctx_get_cache_hints(cwlb_ctx* ctx, int64_t* hot_bytes)
     return CWLB_OK;
 }
 
+cwlb_status cwlb_ctx_last_launch(cwlb_ctx* ctx, cwlb_launch_info* out)
+{
+    if (!ctx || !out) return fail(CWLB_INVALID_ARG, "null argument");
+    *out = ctx->last_launch;
+    return CWLB_OK;
+}
+
 cwlb_status cwlb_spmm_mean_f32(cwlb_ctx* ctx, const int32_t* row_ptr, const int32_t* col_idx,
                                const float* val, const int32_t* origin, int32_t n_rows,
                                int64_t nnz, const float* H, int64_t h_rows, int32_t K,

@@ -116,7 +116,7 @@ unsigned grid_for(long long n)
 }  // namespace
 
 cwlb_status build_cache_hints(cwlb_ctx* ctx, const SpmmArgs& a, long long hot_rows,
-                              const unsigned long long** hints)
+                              bool may_build, const unsigned long long** hints)
 {
     *hints = nullptr;
     if (a.nnz <= 0 || a.h_rows <= 0 || hot_rows <= 0) return CWLB_OK;
@@ -125,6 +125,7 @@ cwlb_status build_cache_hints(cwlb_ctx* ctx, const SpmmArgs& a, long long hot_ro
         *hints = ctx->hint_any_cold ? ctx->d_hints : nullptr;
         return CWLB_OK;
     }
+    if (!may_build) return CWLB_OK;
     ctx->hint_col = nullptr;  // invalid until rebuilt
     hipStream_t st = ctx->stream;
     const long long words = (static_cast<long long>(a.nnz) + 63) / 64;

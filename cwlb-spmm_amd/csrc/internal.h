@@ -61,6 +61,7 @@ struct cwlb_ctx {
     unsigned hint_theta = 0;
     bool hint_any_cold = false;
     bool last_call_hinted = false;  // the last aggregation launch used hints
+    cwlb_launch_info last_launch{};  // the last aggregation launch's schedule
     // Pinned host staging of the host-pointer entry point: two buffers used
     // alternately, each with the event of the last transfer through it.
     void* h_stage[2] = {nullptr, nullptr};
@@ -126,8 +127,10 @@ cwlb_status launch_spmm_mean(cwlb_ctx* ctx, const SpmmArgs& a, bool zero_all, bo
 // M tasks) sorted by the original id of each run's first row, on
 // ctx->stream, unless the order of the same task array, origin array, task
 // count and run length is already there; *order receives ctx->d_run_order.
+// With may_build false (a stream under graph capture) nothing is computed:
+// *order is the kept order when it matches, else null (task order).
 cwlb_status build_run_order(cwlb_ctx* ctx, const SpmmArgs& a, int M, long long n_runs,
-                            const int** order);
+                            bool may_build, const int** order);
 
 // The GPU partition (csrc/partition.hip): row_ptr and out are device
 // arrays; synchronises.
@@ -139,9 +142,10 @@ cwlb_status launch_fill_features(cwlb_ctx* ctx, float* H, int64_t rows, int32_t 
 
 // Builds (or reuses) the per-nonzero cold-column bits for a hot set of
 // hot_rows feature rows (csrc/col_hints.hip); synchronises when it builds.
-// *hints is null when no column is cold.
+// *hints is null when no column is cold, and when the bits would have to be
+// built but may_build is false (a stream under graph capture).
 cwlb_status build_cache_hints(cwlb_ctx* ctx, const SpmmArgs& a, long long hot_rows,
-                              const unsigned long long** hints);
+                              bool may_build, const unsigned long long** hints);
 
 cwlb_status launch_reorder(cwlb_ctx* ctx, int32_t n_rows, int64_t nnz, const int32_t* row_ptr,
                            const int32_t* col_idx, const float* val, int32_t* origin,

@@ -204,7 +204,7 @@ cwlb_status grow(T** p, long long have, long long want)
 }  // namespace
 
 cwlb_status build_run_order(cwlb_ctx* ctx, const SpmmArgs& a, int M, long long n_runs,
-                            const int** order)
+                            bool may_build, const int** order)
 {
     hipStream_t st = ctx->stream;
     if (n_runs <= 0 || a.n_rows <= 0) {
@@ -214,6 +214,10 @@ cwlb_status build_run_order(cwlb_ctx* ctx, const SpmmArgs& a, int M, long long n
     if (ctx->order_tasks == a.tasks && ctx->order_origin == a.origin &&
         ctx->order_n_tasks == a.n_tasks && ctx->order_runs == n_runs && ctx->order_M == M) {
         *order = ctx->d_run_order;
+        return CWLB_OK;
+    }
+    if (!may_build) {
+        *order = nullptr;
         return CWLB_OK;
     }
     ctx->order_runs = -1;

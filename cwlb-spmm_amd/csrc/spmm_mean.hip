@@ -883,13 +883,20 @@ cwlb_status launch_spmm_mean(cwlb_ctx* ctx, const SpmmArgs& a, bool zero_all, bo
         return fail(CWLB_UNSUPPORTED,
                     "spmm: too many runs for one launch (more than 2^32 work-items); use more "
                     "tasks per wave (cwlb_ctx_set_schedule) or a larger S");
+    // Under graph capture the run order and the cache hints are only reused,
+    // never built (building allocates and synchronises); without them the
+    // launch runs in task order with the normal cache policy, which gives
+    // the same results.
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    CWLB_HIP_TRY(hipStreamIsCapturing(st, &capture));
+    const bool may_build = capture == hipStreamCaptureStatusNone;
     // Cache hints: 16-byte lanes, one vector per lane and slice, and the
     // feature matrix addressable by 32-bit byte offsets.
     if (!per_task && ctx->sched_hot_bytes > 0 && p.vec == 4 && a.n_tasks > 0 && a.K > 0 &&
         a.K / p.sl <= 256 &&
         static_cast<unsigned long long>(a.h_rows) * a.K * 4ull <= 0xFFFFFFFFull) {
         const long long hot_rows = ctx->sched_hot_bytes / (4ll * a.K);
-        const cwlb_status s = build_cache_hints(ctx, a, hot_rows, &p.hints);
+        const cwlb_status s = build_cache_hints(ctx, a, hot_rows, may_build, &p.hints);
         if (s != CWLB_OK) return s;
     }
     ctx->last_call_hinted = p.hints != nullptr;
@@ -903,9 +910,16 @@ cwlb_status launch_spmm_mean(cwlb_ctx* ctx, const SpmmArgs& a, bool zero_all, bo
                            std::max<long long>(total, 0), ctx->d_status);
     }
     if (p.ordered && a.n_tasks > 0 && a.K > 0) {
-        const cwlb_status s = build_run_order(ctx, a, p.M, p.runs, &p.order);
+        const cwlb_status s = build_run_order(ctx, a, p.M, p.runs, may_build, &p.order);
         if (s != CWLB_OK) return s;
     }
+    ctx->last_launch.tasks_per_wave = p.M;
+    ctx->last_launch.feature_slices = p.sl;
+    ctx->last_launch.run_order = p.order ? 2 : 1;
+    ctx->last_launch.xcd_blocks = p.chunk > 0 ? 2 : 1;
+    ctx->last_launch.cache_hints = p.hints ? 1 : 0;
+    ctx->last_launch.vector_width = p.vec;
+    ctx->last_launch.grid_blocks = a.n_tasks > 0 && a.K > 0 ? p.grid : 0;
     if (!zero_all && a.n_tasks > 0 && a.K > 0) {
         if (p.vec == 4) launch_zero<4>(st, a, p, ctx->d_status);
         else if (p.vec == 2) launch_zero<2>(st, a, p, ctx->d_status);

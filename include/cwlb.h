@@ -131,8 +131,9 @@ cwlb_status cwlb_ctx_set_locality(cwlb_ctx* ctx, int32_t run_order, int32_t xcd_
  * and the rest are loaded non-temporally, so that on skewed graphs the hot
  * rows stay in L2 and the Infinity Cache.  The first call after a change of
  * the column array, nnz, h_rows or hot_bytes builds one bit per nonzero in a
- * context-owned device buffer (and synchronises the stream; that call cannot
- * be captured into a HIP graph); later calls reuse it.  The hints steer
+ * context-owned device buffer (and synchronises the stream); later calls
+ * reuse it.  A call on a stream under graph capture never builds: it reuses
+ * matching hints or runs without them.  The hints steer
  * only the cache policy: results are the same with or without them, and
  * hints left over from earlier contents of col_idx only cost speed.
  * Applies with 16-byte aligned H and C, K a multiple of 4, at most 256
@@ -141,6 +142,21 @@ cwlb_status cwlb_ctx_set_locality(cwlb_ctx* ctx, int32_t run_order, int32_t xcd_
  * 96 MB. */
 cwlb_status cwlb_ctx_set_cache_hints(cwlb_ctx* ctx, int64_t hot_bytes);
 cwlb_status cwlb_ctx_get_cache_hints(cwlb_ctx* ctx, int64_t* hot_bytes);
+
+/* The schedule the last aggregation launch on this context used, as the
+ * automatic choices and the context's settings resolved it (all zero before
+ * the first launch).  No counterpart in the reference; tests and the bench
+ * report it. */
+typedef struct cwlb_launch_info {
+    int32_t tasks_per_wave;  /* tasks per run (1 with CWLB_SPMM_PER_TASK) */
+    int32_t feature_slices;  /* 1, 2, 4 or 8 */
+    int32_t run_order;       /* 1 task order, 2 sorted by output row */
+    int32_t xcd_blocks;      /* 1 interleaved over the XCDs, 2 contiguous */
+    int32_t cache_hints;     /* 1 when the gathers carried cache hints */
+    int32_t vector_width;    /* floats per load: 4, 2 or 1 */
+    int64_t grid_blocks;     /* work-groups of the aggregation kernel */
+} cwlb_launch_info;
+cwlb_status cwlb_ctx_last_launch(cwlb_ctx* ctx, cwlb_launch_info* out);
 
 /* ------------------------------------------------------------ aggregation
  * C[Origin_local[r]][k] = (sum over the task chunks of row r of
@@ -168,7 +184,10 @@ cwlb_status cwlb_ctx_get_cache_hints(cwlb_ctx* ctx, int64_t* hot_bytes);
  * are then reported by the next cwlb_ctx_synchronize); otherwise the call
  * synchronises.  The default and CWLB_SPMM_ZERO_OUTPUT paths launch kernels
  * only (no memset nodes, no allocation), so an asynchronous call can be
- * captured into a HIP graph; run_order = 2 (cwlb_ctx_set_locality) cannot.
+ * captured into a HIP graph.  Under capture the run order (run_order = 2)
+ * and the cache hints are reused when an earlier call built them for the
+ * same arrays, and otherwise left out (task order, normal cache policy);
+ * the results are the same either way.
  *
  * cwlb_spmm_mean_f32 mirrors spmmKernel: K > max work-group size (1024)
  * returns CWLB_INVALID_ARG (parallelMatrix.cpp:84-88).

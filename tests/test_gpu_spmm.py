@@ -610,6 +610,8 @@ def test_cache_hints_change_no_value(gpu_ctx, K):
                 gpu_ctx.set_cache_hints(hot)
                 C1.fill_(float("nan"))
                 gpu_ctx.spmm(d_rp, d_ci, d_v, d_o, g.n, g.nnz, d_H, g.n, K, d_t, len(p.tasks), C1)
+                # every hot set but the one holding all columns leaves cold ones
+                assert gpu_ctx.last_launch()["cache_hints"] == int(hot < g.n * 4 * K), (hot, m, sl)
                 got = C1.cpu().numpy()
                 check(got, ref32)
                 if (m, sl) == (0, 0):
@@ -832,12 +834,30 @@ def test_async_call_reports_bad_column_at_synchronize(gpu_ctx):
     gpu_ctx.synchronize()
 
 
-@pytest.mark.parametrize("flags", [0, capi.ZERO_OUTPUT], ids=["default", "zero_output"])
-def test_hip_graph_capture_and_replay(gpu_ctx, flags):
+HOT64 = 64 * 4 * 64
+# (flags, (hot bytes, run order) of the eager call, the same for the captured
+# call, (cache hints, run order) the captured launch uses): a captured call
+# reuses the cache hints and run order an eager call built, and runs without
+# them when none match.  The unbuilt hints case changes the hot set between
+# the calls: the caching allocator may hand out the column array of an
+# earlier case at the same address, and hints kept for it would match.
+CAPTURE_CASES = {
+    "default": (0, (0, 0), (0, 0), (0, 1)),
+    "zero_output": (capi.ZERO_OUTPUT, (0, 0), (0, 0), (0, 1)),
+    "cache_hints_built": (0, (HOT64, 0), (HOT64, 0), (1, 1)),
+    "cache_hints_unbuilt": (0, (2 * HOT64, 0), (HOT64, 0), (0, 1)),
+    "run_order_built": (0, (0, 2), (0, 2), (0, 2)),
+    "run_order_unbuilt": (0, (0, 0), (0, 2), (0, 1)),
+}
+
+
+@pytest.mark.parametrize("case", list(CAPTURE_CASES))
+def test_hip_graph_capture_and_replay(gpu_ctx, case):
     """An asynchronous call captured into a HIP graph (torch.cuda.CUDAGraph)
     and replayed several times, with eager work and synchronisations in
     between, gives the eager result on every replay."""
     torch = torch_mod()
+    flags, eager_cfg, capture_cfg, used = CAPTURE_CASES[case]
     g = workloads.small(4, seed=21)
     K = 64
     p = problem(g, SKEWED_COSTS, 9)
@@ -845,8 +865,28 @@ def test_hip_graph_capture_and_replay(gpu_ctx, flags):
     d_t = dev(np.ascontiguousarray(p.tasks, np.int32).reshape(-1))
     H = dev(synth.features(g.n, K, 4))
     C = torch.zeros((g.n, K), dtype=torch.float32, device="cuda")
+    gpu_ctx.set_schedule(4, 0)  # runs of 4 tasks, so that a run order exists
+    try:
+        _capture_and_replay(gpu_ctx, torch, g, K, p, (d_rp, d_ci, d_v, d_o, d_t), H, C, flags,
+                            eager_cfg, capture_cfg, used)
+    finally:
+        gpu_ctx.set_schedule(0, 0)
+        gpu_ctx.set_cache_hints(0)
+        gpu_ctx.set_locality(0, 0)
+
+
+def _capture_and_replay(gpu_ctx, torch, g, K, p, d, H, C, flags, eager_cfg, capture_cfg, used):
+    d_rp, d_ci, d_v, d_o, d_t = d
+    gpu_ctx.set_cache_hints(eager_cfg[0])
+    gpu_ctx.set_locality(eager_cfg[1], 0)
     gpu_ctx.spmm(d_rp, d_ci, d_v, d_o, g.n, g.nnz, H, g.n, K, d_t, len(p.tasks), C, flags=flags)
+    info = gpu_ctx.last_launch()
+    assert (info["cache_hints"], info["run_order"]) == (int(eager_cfg[0] > 0),
+                                                        2 if eager_cfg[1] == 2 else 1), info
     eager = C.clone()
+    gpu_ctx.set_cache_hints(capture_cfg[0])
+    if capture_cfg[1] != eager_cfg[1]:
+        gpu_ctx.set_locality(capture_cfg[1], 0)
     graph = torch.cuda.CUDAGraph()
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
@@ -856,6 +896,8 @@ def test_hip_graph_capture_and_replay(gpu_ctx, flags):
             gpu_ctx.spmm(d_rp, d_ci, d_v, d_o, g.n, g.nnz, H, g.n, K, d_t, len(p.tasks), C,
                          flags=flags, timed=False)
     gpu_ctx.set_stream(torch.cuda.current_stream().cuda_stream)
+    info = gpu_ctx.last_launch()
+    assert (info["cache_hints"], info["run_order"]) == used, info
     torch.cuda.synchronize()
     for i in range(4):
         C.fill_(float("nan") if flags else float(i))
