@@ -407,6 +407,9 @@ cwlb_status cwlb_ctx_tune_schedule(cwlb_ctx* ctx, const int32_t* row_ptr, const 
         if (sl == 1 || (K % (4 * sl) == 0 && K / sl >= 32))
             for (int m : {2, 4, 8, 16, 32, 64}) cands.emplace_back(m, sl);
     const int keep_m = ctx->sched_tasks_per_wave, keep_sl = ctx->sched_slices;
+    // Tuning the hints too: the schedule and placement are chosen without.
+    const long long keep_hot = ctx->sched_hot_bytes;
+    if (locality_out) ctx->sched_hot_bytes = 0;
     float best_us = 0.0f;
     std::pair<int, int> best{0, 0};
     std::vector<float> times(static_cast<size_t>(trials));
@@ -422,6 +425,7 @@ cwlb_status cwlb_ctx_tune_schedule(cwlb_ctx* ctx, const int32_t* row_ptr, const 
         if (st != CWLB_OK) {
             ctx->sched_tasks_per_wave = keep_m;
             ctx->sched_slices = keep_sl;
+            ctx->sched_hot_bytes = keep_hot;
             return st;
         }
         std::sort(times.begin(), times.end());
@@ -464,15 +468,16 @@ cwlb_status cwlb_ctx_tune_schedule(cwlb_ctx* ctx, const int32_t* row_ptr, const 
         if (st != CWLB_OK) {
             ctx->sched_order = keep_order;
             ctx->sched_xcd = keep_xcd;
+            ctx->sched_hot_bytes = keep_hot;
             return st;
         }
         locality_out[0] = best_order;
         locality_out[1] = best_xcd;
         // Cache hints for the winner: hot sets of 24, 48 and 96 MB of
-        // feature rows (the hints are built once per size and kept).
-        const long long keep_hot = ctx->sched_hot_bytes;
+        // feature rows (the hints are built once per size and kept).  The
+        // placement is re-timed first: the minimum over many candidates
+        // above is biased low against a single fresh timing.
         long long best_hot = 0;
-        ctx->sched_hot_bytes = 0;
         st = run_spmm(ctx, a, 0, nullptr);
         for (int t = 0; st == CWLB_OK && t < trials; ++t) {
             cwlb_timing tm{};
@@ -481,7 +486,7 @@ cwlb_status cwlb_ctx_tune_schedule(cwlb_ctx* ctx, const int32_t* row_ptr, const 
         }
         if (st == CWLB_OK) {
             std::sort(times.begin(), times.end());
-            best_us = times[times.size() / 2];  // the placement above, re-timed without hints
+            best_us = times[times.size() / 2];
         }
         for (long long mb : {24ll, 48ll, 96ll}) {
             if (st != CWLB_OK) break;

@@ -228,9 +228,11 @@ cwlb_status cwlb_spmm_mean_f32_large_k(cwlb_ctx* ctx, const int32_t* row_ptr,
  * written there (1, 0 or the context's previous setting = task order kept);
  * then with cache hints of 24, 48 and 96 MB (cwlb_ctx_set_cache_hints), the
  * fastest kept on the context (0 = none; read it with
- * cwlb_ctx_get_cache_hints).  C receives the result.  Synchronises.  No counterpart in the reference,
- * whose one task per work-group has nothing to tune; like its S search, it
- * is meant to run once per graph before timed runs. */
+ * cwlb_ctx_get_cache_hints).  In that mode every timing before the hint
+ * sizes runs without hints, whatever the context held.  C receives the
+ * result.  Synchronises.  No counterpart in the reference, whose one task
+ * per work-group has nothing to tune; like its S search, it is meant to run
+ * once per graph before timed runs. */
 cwlb_status cwlb_ctx_tune_schedule(cwlb_ctx* ctx, const int32_t* row_ptr, const int32_t* col_idx,
                                    const float* val, const int32_t* origin, int32_t n_rows,
                                    int64_t nnz, const float* H, int64_t h_rows, int32_t K,

@@ -912,7 +912,8 @@ def _capture_and_replay(gpu_ctx, torch, g, K, p, d, H, C, flags, eager_cfg, capt
 
 def test_tune_schedule(gpu_ctx):
     """cwlb_ctx_tune_schedule picks one of its candidates, leaves it on the
-    context, and every schedule it tried computes the same result."""
+    context, and every schedule it tried computes the same result.  A hot
+    set the context held before is replaced by one of the tuner's sizes."""
     g = workloads.small(4, seed=13)
     K = 128
     p = problem(g, SKEWED_COSTS, 16)
@@ -922,6 +923,7 @@ def test_tune_schedule(gpu_ctx):
     d_t = dev(np.ascontiguousarray(p.tasks, np.int32).reshape(-1))
     d_H = dev(H)
     C = torch.full((g.n, K), float("nan"), dtype=torch.float32, device="cuda")
+    gpu_ctx.set_cache_hints(7 << 20)
     try:
         m, sl, loc = gpu_ctx.tune_schedule(d_rp, d_ci, d_v, d_o, g.n, g.nnz, d_H, g.n, K, d_t,
                                            len(p.tasks), C, trials=2, locality=True)
@@ -934,6 +936,11 @@ def test_tune_schedule(gpu_ctx):
         gpu_ctx.spmm(d_rp, d_ci, d_v, d_o, g.n, g.nnz, d_H, g.n, K, d_t, len(p.tasks), C)
         check(C.cpu().numpy(), ref32)
         check(C.cpu().numpy(), ref64)
+        info = gpu_ctx.last_launch()
+        assert info["cache_hints"] == int(gpu_ctx.cache_hints() > 0), info
+        assert (info["feature_slices"] == sl) if sl else True, info
+        assert (info["tasks_per_wave"] == m) if m else True, info
+        assert info["run_order"] == (2 if loc[0] == 2 else 1), info
         with pytest.raises(capi.CwlbError) as e:
             gpu_ctx.tune_schedule(d_rp, d_ci, d_v, d_o, g.n, g.nnz, d_H, g.n, K, d_t,
                                   len(p.tasks), C, trials=0)
