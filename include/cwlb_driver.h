@@ -71,6 +71,8 @@ struct SingleSResult {
     // Launch schedule the timed launches ran with: tasks per wave, feature
     // slices, run order, XCD placement (all 0 = the automatic schedule).
     std::array<int, 4> schedule{};
+    // Cache-hint hot set in bytes the timed launches ran with (0 = none).
+    std::int64_t cache_hint_bytes = 0;
 };
 
 // Builds the tasks for S (on the GPU, identical to the host partition), then
