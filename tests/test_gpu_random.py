@@ -1,0 +1,102 @@
+"""Seeded random cross-product of graph family, K, S, costs and launch
+schedule (run length, feature slices, run order, XCD placement, cache hints,
+flags, feature-view alignment) against the oracle.
+
+The structured tests in test_gpu_spmm.py cover each setting on fixed graphs;
+these cases draw combinations that no structured test names, with the same
+bar: every output row within 1e-5 relative / 1e-6 absolute of the oracle in
+the reference's value order, and the schedule the library reports for the
+launch consistent with the settings.  The reference's kernel is
+src/parallelMatrix.cpp:63-254 (K <= 1024) and :264-683 (larger K).
+"""
+import numpy as np
+import pytest
+
+import oracle
+from conftest import SKEWED_COSTS, UNIT_COSTS
+from cwlb_amd import capi, synth, workloads
+
+pytestmark = pytest.mark.gpu
+
+RTOL, ATOL = 1e-5, 1e-6
+N_CASES = 192
+K_CHOICES = [1, 2, 3, 4, 7, 8, 12, 16, 31, 32, 48, 60, 64, 96, 100, 128, 200, 256, 300, 384,
+             512, 600, 1024, 1028, 1100]
+
+
+def draw_case(i):
+    """The i-th case: a dict of every setting, reproducible from i alone."""
+    r = np.random.default_rng(1000 + i)
+    costs = [UNIT_COSTS, SKEWED_COSTS,
+             tuple(float(x) for x in np.round(r.uniform(0.05, 4.0, 4), 3))][int(r.integers(3))]
+    return {
+        "family": int(r.integers(1, 6)),
+        "seed": int(r.integers(1, 1 << 20)),
+        "K": K_CHOICES[int(r.integers(len(K_CHOICES)))],
+        "S": int(np.exp(r.uniform(0, np.log(400)))),
+        "costs": costs,
+        "M": [0, 1, 2, 3, 4, 7, 8, 16, 32, 64][int(r.integers(10))],
+        "SL": [0, 1, 2, 4, 8][int(r.integers(5))],
+        "order": int(r.integers(3)),
+        "xcd": int(r.integers(3)),
+        "hot_rows": [0, 0, 16, 256, 4096][int(r.integers(5))],
+        "flags": [0, 0, 0, capi.ZERO_OUTPUT, capi.PER_TASK][int(r.integers(5))],
+        "h_offset": [0, 0, 0, 1, 2][int(r.integers(5))],  # floats past the allocation start
+    }
+
+
+@pytest.mark.parametrize("i", range(N_CASES))
+def test_random_schedule_case(gpu_ctx, i):
+    import torch
+    c = draw_case(i)
+    print(f"case {i}: {c}", flush=True)
+    g = workloads.small(c["family"], seed=c["seed"])
+    K = c["K"]
+    p = workloads.prepare(g, c["costs"], c["S"])
+    H = synth.features(g.n, K, c["seed"] % 997)
+    large_k = K > 1024
+
+    d_rp = torch.from_numpy(p.row_ptr).cuda()
+    d_ci = torch.from_numpy(p.col_idx).cuda()
+    d_v = torch.from_numpy(p.val).cuda()
+    d_o = torch.from_numpy(p.origin).cuda()
+    d_t = torch.from_numpy(np.ascontiguousarray(p.tasks, np.int32).reshape(-1)).cuda()
+    # A feature view starting h_offset floats past a 256-byte boundary.
+    flat = torch.empty(g.n * K + 4, dtype=torch.float32, device="cuda")
+    d_H = flat[c["h_offset"]:c["h_offset"] + g.n * K].view(g.n, K)
+    d_H.copy_(torch.from_numpy(H))
+    C = torch.full((g.n, K), float("nan"), dtype=torch.float32, device="cuda")
+
+    gpu_ctx.set_schedule(c["M"], c["SL"])
+    gpu_ctx.set_locality(c["order"], c["xcd"])
+    gpu_ctx.set_cache_hints(c["hot_rows"] * 4 * K)
+    try:
+        gpu_ctx.spmm(d_rp, d_ci, d_v, d_o, g.n, g.nnz, d_H, g.n, K, d_t, len(p.tasks), C,
+                     flags=c["flags"], large_k=large_k)
+        info = gpu_ctx.last_launch()
+    finally:
+        gpu_ctx.set_schedule(0, 0)
+        gpu_ctx.set_locality(0, 0)
+        gpu_ctx.set_cache_hints(0)
+
+    ref = oracle.spmm_mean_f32(p.row_ptr, p.col_idx, p.val, p.origin, H, p.tasks)
+    np.testing.assert_allclose(C.cpu().numpy(), ref, rtol=RTOL, atol=ATOL, err_msg=str(c))
+
+    per_task = bool(c["flags"] & capi.PER_TASK)
+    if len(p.tasks) and K:
+        assert info["grid_blocks"] > 0, info
+    if per_task:
+        assert (info["tasks_per_wave"], info["feature_slices"]) == (1, 1), info
+        assert (info["run_order"], info["cache_hints"]) == (1, 0), info
+    elif c["M"]:
+        assert info["tasks_per_wave"] == c["M"], info
+    if c["SL"] and not per_task:
+        aligned = info["vector_width"] == 4 and K % (4 * c["SL"]) == 0
+        assert info["feature_slices"] == (c["SL"] if aligned else 1), (info, c)
+    if c["hot_rows"] == 0:
+        assert info["cache_hints"] == 0, info
+    if c["order"] != 2:
+        assert info["run_order"] == 1, info
+    expect_vec = 4 if K % 4 == 0 and c["h_offset"] % 4 == 0 else (
+        2 if K % 2 == 0 and c["h_offset"] % 2 == 0 else 1)
+    assert info["vector_width"] == expect_vec, info
