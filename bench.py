@@ -89,6 +89,7 @@ def segment_size_sweep(ctx, call, tune, dev, tasks_for, cfg, costs, S, trials):
     ctx.set_schedule(0, 0)
     ctx.set_locality(0, 0)
     ctx.set_cache_hints(0)
+    ctx.set_occupancy(0)
     for _ in range(3):
         call(d_t, len(tk), False)
     auto_us = float(np.mean([call(d_t, len(tk), True).main_us for _ in range(trials)]))
@@ -99,7 +100,8 @@ def segment_size_sweep(ctx, call, tune, dev, tasks_for, cfg, costs, S, trials):
     return {"S": S, "tasks": int(len(tk)), "automatic_us": round(auto_us, 1),
             "tuned_us": round(tuned_us, 1),
             "schedule": {"tasks_per_wave": m, "feature_slices": sl, "run_order": order,
-                         "xcd_blocks": xcd, "hot_bytes": ctx.cache_hints()},
+                         "xcd_blocks": xcd, "hot_bytes": ctx.cache_hints(),
+                         "occupancy": ctx.occupancy()},
             "tasks_match_reference_fixture": reference_partition_match(cfg, S, costs, tk)}
 
 
@@ -162,6 +164,8 @@ def main():
     ap.add_argument("--tasks-per-wave", type=int, default=0,
                     help="fixed launch schedule (with --slices) instead of tuning")
     ap.add_argument("--slices", type=int, default=0)
+    ap.add_argument("--occupancy", type=int, default=0, choices=(0, 6),
+                    help="fixed schedule: 6 = the 6-waves-per-SIMD kernel variant")
     ap.add_argument("--run-order", type=int, default=0,
                     help="fixed run order (cwlb_ctx_set_locality: 1 task order, 2 by output row)")
     ap.add_argument("--xcd-blocks", type=int, default=0,
@@ -249,19 +253,21 @@ def main():
     # (cwlb_ctx_tune_schedule; 0, 0 = the automatic choice won).
     schedule = {"tasks_per_wave": 0, "feature_slices": 0, "tuned": False,
                 "automatic_schedule_us": round(float(auto_us), 1)}
-    if args.tasks_per_wave or args.slices or args.run_order or args.xcd_blocks or args.hot_mb:
+    if (args.tasks_per_wave or args.slices or args.run_order or args.xcd_blocks or args.hot_mb
+            or args.occupancy):
         ctx.set_schedule(args.tasks_per_wave, args.slices)
         ctx.set_locality(args.run_order, args.xcd_blocks)
         ctx.set_cache_hints(args.hot_mb << 20)
+        ctx.set_occupancy(args.occupancy)
         schedule.update(tasks_per_wave=args.tasks_per_wave, feature_slices=args.slices,
                         run_order=args.run_order, xcd_blocks=args.xcd_blocks,
-                        hot_bytes=args.hot_mb << 20)
+                        hot_bytes=args.hot_mb << 20, occupancy=args.occupancy)
         log(f"fixed schedule: {schedule}")
     elif not args.no_tune:
         t0 = time.perf_counter()
         m, sl, (order, xcd) = tune(d_t, T)
         schedule.update(tasks_per_wave=m, feature_slices=sl, run_order=order, xcd_blocks=xcd,
-                        hot_bytes=ctx.cache_hints(), tuned=True,
+                        hot_bytes=ctx.cache_hints(), occupancy=ctx.occupancy(), tuned=True,
                         tuning_ms=round((time.perf_counter() - t0) * 1e3, 1))
         log(f"tuned schedule: {schedule}")
 
@@ -319,6 +325,7 @@ def main():
         ctx.set_schedule(0, 0)
         ctx.set_locality(0, 0)
         ctx.set_cache_hints(0)
+        ctx.set_occupancy(0)
 
     flops = 2.0 * g.nnz * K
     gflops = flops / (ms_per_step * 1e-3) / 1e9

@@ -367,6 +367,22 @@ cwlb_status cwlb_ctx_get_cache_hints(cwlb_ctx* ctx, int64_t* hot_bytes)
     return CWLB_OK;
 }
 
+cwlb_status cwlb_ctx_set_occupancy(cwlb_ctx* ctx, int32_t waves_per_simd)
+{
+    if (!ctx) return fail(CWLB_INVALID_ARG, "null context");
+    if (waves_per_simd != 0 && waves_per_simd != 6)
+        return fail(CWLB_INVALID_ARG, "waves_per_simd must be 0 (standard kernel) or 6");
+    ctx->sched_occupancy = waves_per_simd;
+    return CWLB_OK;
+}
+
+cwlb_status cwlb_ctx_get_occupancy(cwlb_ctx* ctx, int32_t* waves_per_simd)
+{
+    if (!ctx || !waves_per_simd) return fail(CWLB_INVALID_ARG, "null argument");
+    *waves_per_simd = ctx->sched_occupancy;
+    return CWLB_OK;
+}
+
 cwlb_status cwlb_ctx_last_launch(cwlb_ctx* ctx, cwlb_launch_info* out)
 {
     if (!ctx || !out) return fail(CWLB_INVALID_ARG, "null argument");
@@ -407,55 +423,79 @@ cwlb_status cwlb_ctx_tune_schedule(cwlb_ctx* ctx, const int32_t* row_ptr, const 
         if (sl == 1 || (K % (4 * sl) == 0 && K / sl >= 32))
             for (int m : {2, 4, 8, 16, 32, 64}) cands.emplace_back(m, sl);
     const int keep_m = ctx->sched_tasks_per_wave, keep_sl = ctx->sched_slices;
-    // Tuning the hints too: the schedule and placement are chosen without.
+    // Tuning the hints and the occupancy variant too: the schedule and
+    // placement are chosen without them.
     const long long keep_hot = ctx->sched_hot_bytes;
-    if (locality_out) ctx->sched_hot_bytes = 0;
+    const int keep_occ = ctx->sched_occupancy;
+    if (locality_out) {
+        ctx->sched_hot_bytes = 0;
+        ctx->sched_occupancy = 0;
+    }
     float best_us = 0.0f;
     std::pair<int, int> best{0, 0};
     std::vector<float> times(static_cast<size_t>(trials));
+    // One warm-up, then the median of `trials` event-timed calls under the
+    // context's current settings.  The warm-up builds what the settings
+    // need (run order, hints); `applies` (optional) reads the warm-up's
+    // launch and skips the timing when it returns false.
+    auto time_current = [&](float* med, bool (*applies)(const cwlb_ctx*)) -> cwlb_status {
+        cwlb_status s = run_spmm(ctx, a, 0, nullptr);
+        if (s != CWLB_OK) return s;
+        if (applies && !applies(ctx)) {
+            *med = 0.0f;
+            return CWLB_OK;
+        }
+        for (int t = 0; t < trials; ++t) {
+            cwlb_timing tm{};
+            s = run_spmm(ctx, a, 0, &tm);
+            if (s != CWLB_OK) return s;
+            times[static_cast<size_t>(t)] = tm.total_us;
+        }
+        std::sort(times.begin(), times.end());
+        *med = times[times.size() / 2];
+        return CWLB_OK;
+    };
+    auto restore = [&](int order, int xcd) {
+        ctx->sched_tasks_per_wave = keep_m;
+        ctx->sched_slices = keep_sl;
+        ctx->sched_order = order;
+        ctx->sched_xcd = xcd;
+        ctx->order_runs = -1;
+        ctx->sched_hot_bytes = keep_hot;
+        ctx->sched_occupancy = keep_occ;
+    };
+    const int keep_order = ctx->sched_order, keep_xcd = ctx->sched_xcd;
     for (const auto& c : cands) {
         ctx->sched_tasks_per_wave = c.first;
         ctx->sched_slices = c.second;
-        st = run_spmm(ctx, a, 0, nullptr);  // warm-up
-        for (int t = 0; st == CWLB_OK && t < trials; ++t) {
-            cwlb_timing tm{};
-            st = run_spmm(ctx, a, 0, &tm);
-            times[static_cast<size_t>(t)] = tm.total_us;
-        }
+        float med = 0.0f;
+        st = time_current(&med, nullptr);
         if (st != CWLB_OK) {
-            ctx->sched_tasks_per_wave = keep_m;
-            ctx->sched_slices = keep_sl;
-            ctx->sched_hot_bytes = keep_hot;
+            restore(keep_order, keep_xcd);
             return st;
         }
-        std::sort(times.begin(), times.end());
-        const float med = times[times.size() / 2];
         if (best_us == 0.0f || med < best_us) {
             best_us = med;
             best = c;
         }
     }
-    // Locality placements for the best schedule: runs sorted by output row
-    // (the order is computed once and reused), with interleaved or
-    // contiguous XCD stretches.
-    const int keep_order = ctx->sched_order, keep_xcd = ctx->sched_xcd;
     ctx->sched_tasks_per_wave = best.first;
     ctx->sched_slices = best.second;
-    int best_order = keep_order, best_xcd = keep_xcd;
     if (locality_out) {
+        // Locality placements for the best schedule: runs sorted by output
+        // row (the order is computed once and reused), with interleaved or
+        // contiguous XCD stretches.
+        int best_order = keep_order, best_xcd = keep_xcd;
         for (const auto& loc : {std::pair<int, int>{2, 1}, {2, 2}}) {
             ctx->sched_order = loc.first;
             ctx->sched_xcd = loc.second;
             ctx->order_runs = -1;
-            st = run_spmm(ctx, a, 0, nullptr);  // warm-up, builds the order
-            for (int t = 0; st == CWLB_OK && t < trials; ++t) {
-                cwlb_timing tm{};
-                st = run_spmm(ctx, a, 0, &tm);
-                times[static_cast<size_t>(t)] = tm.total_us;
+            float med = 0.0f;
+            st = time_current(&med, nullptr);
+            if (st != CWLB_OK) {
+                restore(keep_order, keep_xcd);
+                return st;
             }
-            if (st != CWLB_OK) break;
-            std::sort(times.begin(), times.end());
-            const float med = times[times.size() / 2];
             if (med < best_us) {
                 best_us = med;
                 best_order = loc.first;
@@ -465,51 +505,76 @@ cwlb_status cwlb_ctx_tune_schedule(cwlb_ctx* ctx, const int32_t* row_ptr, const 
         ctx->sched_order = best_order;
         ctx->sched_xcd = best_xcd;
         ctx->order_runs = -1;
-        if (st != CWLB_OK) {
-            ctx->sched_order = keep_order;
-            ctx->sched_xcd = keep_xcd;
-            ctx->sched_hot_bytes = keep_hot;
-            return st;
-        }
         locality_out[0] = best_order;
         locality_out[1] = best_xcd;
-        // Cache hints for the winner: hot sets of 24, 48 and 96 MB of
-        // feature rows (the hints are built once per size and kept).  The
-        // placement is re-timed first: the minimum over many candidates
-        // above is biased low against a single fresh timing.
-        long long best_hot = 0;
-        st = run_spmm(ctx, a, 0, nullptr);
-        for (int t = 0; st == CWLB_OK && t < trials; ++t) {
-            cwlb_timing tm{};
-            st = run_spmm(ctx, a, 0, &tm);
-            times[static_cast<size_t>(t)] = tm.total_us;
-        }
+        // Then, one at a time, the occupancy variant and the cache hints
+        // (hot sets of 24, 48 and 96 MB of feature rows; the hints are built
+        // once per size and kept), each kept when faster than the current
+        // settings.  The current settings are re-timed before each: the
+        // minimum over many candidates above is biased low against a single
+        // fresh timing.
+        float base = 0.0f;
+        const int m_standard = best.first;
+        st = time_current(&base, nullptr);
         if (st == CWLB_OK) {
-            std::sort(times.begin(), times.end());
-            best_us = times[times.size() / 2];
+            ctx->sched_occupancy = 6;
+            float med = 0.0f;
+            st = time_current(&med, [](const cwlb_ctx* c) { return c->last_launch.waves_per_simd == 6; });
+            if (st == CWLB_OK && !(med > 0.0f && med < base)) ctx->sched_occupancy = 0;
+            if (st == CWLB_OK && ctx->sched_occupancy == 6) {
+                // More waves in flight can move the best run length: its
+                // neighbours (half and double) under the variant.
+                base = med;
+                const int m0 = best.first;
+                for (int m : {m0 / 2, m0 * 2}) {
+                    if (st != CWLB_OK || m0 == 0 || m < 1 || m > 64) continue;
+                    ctx->sched_tasks_per_wave = m;
+                    st = time_current(&med, nullptr);
+                    if (st == CWLB_OK && med < base) {
+                        base = med;
+                        best.first = m;
+                    }
+                }
+                ctx->sched_tasks_per_wave = best.first;
+            }
         }
+        if (st == CWLB_OK) st = time_current(&base, nullptr);
+        long long best_hot = 0;
         for (long long mb : {24ll, 48ll, 96ll}) {
             if (st != CWLB_OK) break;
             ctx->sched_hot_bytes = mb << 20;
-            st = run_spmm(ctx, a, 0, nullptr);  // warm-up, builds the hints
+            float med = 0.0f;
             // Hints that do not apply to this call (K, alignment, H size) or
             // mark no column cold leave nothing to time.
-            if (st != CWLB_OK || !ctx->last_call_hinted) break;
-            for (int t = 0; st == CWLB_OK && t < trials; ++t) {
-                cwlb_timing tm{};
-                st = run_spmm(ctx, a, 0, &tm);
-                times[static_cast<size_t>(t)] = tm.total_us;
-            }
-            if (st != CWLB_OK) break;
-            std::sort(times.begin(), times.end());
-            const float med = times[times.size() / 2];
-            if (med < best_us) {
-                best_us = med;
+            st = time_current(&med, [](const cwlb_ctx* c) { return c->last_call_hinted; });
+            if (st != CWLB_OK || med == 0.0f) break;
+            if (med < base) {
+                base = med;
                 best_hot = mb << 20;
             }
         }
-        ctx->sched_hot_bytes = st == CWLB_OK ? best_hot : keep_hot;
-        if (st != CWLB_OK) return st;
+        ctx->sched_hot_bytes = best_hot;
+        if (st == CWLB_OK && ctx->sched_occupancy == 6) {
+            // The variant was chosen without hints: with the chosen hints
+            // the standard kernel (at its own run length) can be faster.
+            // Both are timed afresh, one after the other.
+            const int m6 = best.first;
+            if (best_hot) st = time_current(&base, nullptr);
+            ctx->sched_occupancy = 0;
+            ctx->sched_tasks_per_wave = m_standard;
+            float med = 0.0f;
+            if (st == CWLB_OK) st = time_current(&med, nullptr);
+            if (st == CWLB_OK && med < base) {
+                best.first = m_standard;
+            } else {
+                ctx->sched_occupancy = 6;
+                ctx->sched_tasks_per_wave = m6;
+            }
+        }
+        if (st != CWLB_OK) {
+            restore(keep_order, keep_xcd);
+            return st;
+        }
     }
     if (tasks_per_wave_out) *tasks_per_wave_out = best.first;
     if (feature_slices_out) *feature_slices_out = best.second;

@@ -29,6 +29,7 @@ struct cwlb_ctx {
     int sched_slices = 0;
     int sched_order = 0;
     int sched_xcd = 0;
+    int sched_occupancy = 0;  // 0 standard kernel, 6 the 6-waves-per-SIMD variant
     // Grow-only device buffers for the run order: keys, sorted keys, the
     // order itself and the sort's temporary storage.
     unsigned* d_run_keys = nullptr;

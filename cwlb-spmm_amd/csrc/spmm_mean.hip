@@ -28,6 +28,9 @@
 //     per-work-item loop);
 //   * a long chunk runs on all slots at once, UL nonzeros in flight per
 //     slot, followed by a shuffle reduction across slots;
+//   * the occupancy variant (O6) keeps UL <= 2, which lets slots of 4 to 16
+//     lanes fit 80 VGPRs: 6 waves per SIMD instead of 5, for graphs of
+//     short rows, where waves in flight set the speed;
 //   * column indices and values are fetched with coalesced streaming loads:
 //     64 at a time for a long chunk, handed to the slots with cross-lane
 //     shuffles; for a group of short rows, the group's whole contiguous
@@ -284,8 +287,8 @@ __device__ __forceinline__ void block_slice(int& slice, long long& jb, long long
                    : static_cast<long long>(bx >> 3) * P + q;
 }
 
-template <int VEC, int G, int R, int U, int SL, bool HN>
-__global__ void __launch_bounds__(kBlock)
+template <int VEC, int G, int R, int U, int SL, bool HN, bool O6>
+__global__ void __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(O6 ? 6 : 1)))
 spmm_mean_runs(const int* __restrict__ rp, const int* __restrict__ ci,
                const float* __restrict__ val, const int* __restrict__ origin, int n_rows,
                long long nnz, const float* __restrict__ H, long long h_rows, int ld,
@@ -299,7 +302,8 @@ spmm_mean_runs(const int* __restrict__ rp, const int* __restrict__ ci,
     constexpr int NS = 64 / G;                     // row slots per wave
     constexpr int RU = cmin(cmin(U, 4), G);        // rows per slot (short rows)
     constexpr int GROUP = NS * RU;                 // rows per short-row group (<= 64)
-    constexpr int UL = cmin(U, G);                 // nonzeros per slot per step (long rows)
+    // nonzeros per slot per step (long rows)
+    constexpr int UL = O6 ? cmin(cmin(U, G), 2) : cmin(U, G);
     constexpr int STEP = NS * UL;                  // nonzeros per wave step (<= 64)
     constexpr int kLong = GROUP > 2 ? GROUP : 2;   // chunk length that runs on all slots
     // A short-row group holds at most GROUP * (kLong - 1) nonzeros.  When
@@ -716,15 +720,16 @@ struct Plan {
     long long chunk;       // run blocks per XCD when contiguous, else 0
     long long grid;        // launched blocks
     bool ordered;          // runs execute sorted by output row id
+    bool o6;               // the 6-waves-per-SIMD variant
     const int* order;      // that order (device), set at launch
     const unsigned long long* hints;  // cold-column bits (device) or null
 };
 
-template <int VEC, int G, int R, int SL, bool HN = false>
+template <int VEC, int G, int R, int SL, bool HN = false, bool O6 = false>
 void launch_main(hipStream_t st, const SpmmArgs& a, const Plan& p, int* status)
 {
     constexpr int U = (R == 1) ? 8 : (R == 2) ? 4 : (R <= 4) ? 2 : 1;
-    hipLaunchKernelGGL((spmm_mean_runs<VEC, G, R, U, SL, HN>),
+    hipLaunchKernelGGL((spmm_mean_runs<VEC, G, R, U, SL, HN, O6>),
                        dim3(static_cast<unsigned>(p.grid)), dim3(kBlock), 0, st, a.row_ptr,
                        a.col_idx, a.val, a.origin, a.n_rows, static_cast<long long>(a.nnz), a.H,
                        static_cast<long long>(a.h_rows), a.K, a.tasks,
@@ -747,6 +752,17 @@ void dispatch_hinted(hipStream_t st, const SpmmArgs& a, const Plan& p, int* stat
     }
 }
 
+// The occupancy variant: slots of 4, 8 or 16 lanes of 16 bytes.
+template <int SL, bool HN>
+void dispatch_o6(hipStream_t st, const SpmmArgs& a, const Plan& p, int* status, int G)
+{
+    switch (G) {
+    case 4: return launch_main<4, 4, 1, SL, HN, true>(st, a, p, status);
+    case 8: return launch_main<4, 8, 1, SL, HN, true>(st, a, p, status);
+    default: return launch_main<4, 16, 1, SL, HN, true>(st, a, p, status);
+    }
+}
+
 template <int VEC, int SL>
 void dispatch_width(hipStream_t st, const SpmmArgs& a, const Plan& p, int* status)
 {
@@ -755,6 +771,10 @@ void dispatch_width(hipStream_t st, const SpmmArgs& a, const Plan& p, int* statu
         int G = 1;
         while (G < F) G <<= 1;
         if constexpr (VEC == 4) {
+            if (p.o6 && G >= 4 && G <= 16) {
+                if (p.hints) return dispatch_o6<SL, true>(st, a, p, status, G);
+                return dispatch_o6<SL, false>(st, a, p, status, G);
+            }
             if (p.hints) return dispatch_hinted<VEC, SL>(st, a, p, status, G);
         }
         switch (G) {
@@ -866,6 +886,11 @@ Plan make_plan(const cwlb_ctx* ctx, const SpmmArgs& a, bool per_task)
         p.M *= 2;
     }
     p.ordered = !per_task && ctx->sched_order == 2 && p.runs > 1;
+    // The occupancy variant exists for 16-byte lanes and slots of 4 to 16
+    // lanes (more than 8 and at most 64 floats per feature slice).
+    const int f4 = a.K / p.sl / 4;
+    p.o6 = !per_task && ctx->sched_occupancy == 6 && p.vec == 4 && a.K % (4 * p.sl) == 0 &&
+           f4 > 2 && f4 <= 16;
     p.order = nullptr;
     p.hints = nullptr;
     return p;
@@ -919,6 +944,7 @@ cwlb_status launch_spmm_mean(cwlb_ctx* ctx, const SpmmArgs& a, bool zero_all, bo
     ctx->last_launch.xcd_blocks = p.chunk > 0 ? 2 : 1;
     ctx->last_launch.cache_hints = p.hints ? 1 : 0;
     ctx->last_launch.vector_width = p.vec;
+    ctx->last_launch.waves_per_simd = p.o6 ? 6 : 0;
     ctx->last_launch.grid_blocks = a.n_tasks > 0 && a.K > 0 ? p.grid : 0;
     if (!zero_all && a.n_tasks > 0 && a.K > 0) {
         if (p.vec == 4) launch_zero<4>(st, a, p, ctx->d_status);

@@ -24,7 +24,7 @@ EXPORTS = [
     "cwlb_version", "cwlb_last_error", "cwlb_ctx_create", "cwlb_ctx_destroy",
     "cwlb_ctx_set_stream", "cwlb_ctx_synchronize", "cwlb_ctx_device_info", "cwlb_ctx_set_schedule",
     "cwlb_ctx_set_locality", "cwlb_ctx_set_cache_hints", "cwlb_ctx_get_cache_hints",
-    "cwlb_ctx_last_launch",
+    "cwlb_ctx_last_launch", "cwlb_ctx_set_occupancy", "cwlb_ctx_get_occupancy",
     "cwlb_ctx_tune_schedule",
     "cwlb_spmm_mean_f32", "cwlb_spmm_mean_f32_large_k", "cwlb_spmm_mean_f32_host",
     "cwlb_reorder_by_degree", "cwlb_reorder_by_degree_device", "cwlb_partition",
@@ -71,6 +71,7 @@ class LaunchInfo(C.Structure):
     _fields_ = [("tasks_per_wave", C.c_int32), ("feature_slices", C.c_int32),
                 ("run_order", C.c_int32), ("xcd_blocks", C.c_int32),
                 ("cache_hints", C.c_int32), ("vector_width", C.c_int32),
+                ("waves_per_simd", C.c_int32), ("reserved", C.c_int32),
                 ("grid_blocks", C.c_int64)]
 
 
@@ -111,6 +112,8 @@ def lib():
         L.cwlb_ctx_set_cache_hints.argtypes = [vp, i64]
         L.cwlb_ctx_get_cache_hints.argtypes = [vp, C.POINTER(i64)]
         L.cwlb_ctx_last_launch.argtypes = [vp, C.POINTER(LaunchInfo)]
+        L.cwlb_ctx_set_occupancy.argtypes = [vp, i32]
+        L.cwlb_ctx_get_occupancy.argtypes = [vp, C.POINTER(i32)]
         L.cwlb_ctx_tune_schedule.argtypes = [vp, vp, vp, vp, vp, i32, i64, vp, i64, i32, vp, i64,
                                              vp, i32, C.POINTER(i32), C.POINTER(i32), vp]
         spmm = [vp, vp, vp, vp, vp, i32, i64, vp, i64, i32, vp, i64, vp, u32, C.POINTER(Timing)]
@@ -290,7 +293,16 @@ class Context:
         """The schedule of the last aggregation launch, as a dict."""
         info = LaunchInfo()
         check(lib().cwlb_ctx_last_launch(self.h, C.byref(info)))
-        return {name: getattr(info, name) for name, _ in LaunchInfo._fields_}
+        return {name: getattr(info, name) for name, _ in LaunchInfo._fields_
+                if name != "reserved"}
+
+    def set_occupancy(self, waves_per_simd=0):
+        check(lib().cwlb_ctx_set_occupancy(self.h, int(waves_per_simd)))
+
+    def occupancy(self):
+        v = i32()
+        check(lib().cwlb_ctx_get_occupancy(self.h, C.byref(v)))
+        return v.value
 
     def tune_schedule(self, row_ptr, col_idx, val, origin, n_rows, nnz, H, h_rows, K, tasks,
                       n_tasks, C_out, trials=3, locality=False):

@@ -143,6 +143,18 @@ cwlb_status cwlb_ctx_set_locality(cwlb_ctx* ctx, int32_t run_order, int32_t xcd_
 cwlb_status cwlb_ctx_set_cache_hints(cwlb_ctx* ctx, int64_t hot_bytes);
 cwlb_status cwlb_ctx_get_cache_hints(cwlb_ctx* ctx, int64_t* hot_bytes);
 
+/* Kernel occupancy of later SpMM calls on this context.  waves_per_simd = 0
+ * (the default): the standard kernel, 5 waves per SIMD where its slots are
+ * wider than 2 lanes.  6: a variant with at most 2 nonzeros per slot in
+ * flight on long chunks, which fits 80 VGPRs and runs 6 waves per SIMD;
+ * faster on graphs of short rows (latency-bound), slower on graphs with
+ * hub rows.  It applies to 16-byte lanes with more than 8 and at most 64
+ * floats per feature slice; otherwise the standard kernel runs.  Results
+ * are the same within the documented tolerance (full short rows bit for
+ * bit).  No counterpart in the reference; cwlb_ctx_tune_schedule tries it. */
+cwlb_status cwlb_ctx_set_occupancy(cwlb_ctx* ctx, int32_t waves_per_simd);
+cwlb_status cwlb_ctx_get_occupancy(cwlb_ctx* ctx, int32_t* waves_per_simd);
+
 /* The schedule the last aggregation launch on this context used, as the
  * automatic choices and the context's settings resolved it (all zero before
  * the first launch).  No counterpart in the reference; tests and the bench
@@ -154,6 +166,8 @@ typedef struct cwlb_launch_info {
     int32_t xcd_blocks;      /* 1 interleaved over the XCDs, 2 contiguous */
     int32_t cache_hints;     /* 1 when the gathers carried cache hints */
     int32_t vector_width;    /* floats per load: 4, 2 or 1 */
+    int32_t waves_per_simd;  /* 6 for the occupancy variant, else 0 */
+    int32_t reserved;
     int64_t grid_blocks;     /* work-groups of the aggregation kernel */
 } cwlb_launch_info;
 cwlb_status cwlb_ctx_last_launch(cwlb_ctx* ctx, cwlb_launch_info* out);
@@ -226,10 +240,13 @@ cwlb_status cwlb_spmm_mean_f32_large_k(cwlb_ctx* ctx, const int32_t* row_ptr,
  * also timed with runs sorted by output row (interleaved and contiguous XCD
  * placement, cwlb_ctx_set_locality), the winner is kept on the context and
  * written there (1, 0 or the context's previous setting = task order kept);
- * then with cache hints of 24, 48 and 96 MB (cwlb_ctx_set_cache_hints), the
+ * then with the occupancy variant (cwlb_ctx_set_occupancy, kept when
+ * faster, and then also timed at half and double the run length, so the
+ * tasks per wave returned can be 1); then with cache hints of 24, 48 and 96 MB (cwlb_ctx_set_cache_hints), the
  * fastest kept on the context (0 = none; read it with
  * cwlb_ctx_get_cache_hints).  In that mode every timing before the hint
- * sizes runs without hints, whatever the context held.  C receives the
+ * sizes runs without hints, and every timing before the occupancy variant
+ * with the standard kernel, whatever the context held.  C receives the
  * result.  Synchronises.  No counterpart in the reference, whose one task
  * per work-group has nothing to tune; like its S search, it is meant to run
  * once per graph before timed runs. */

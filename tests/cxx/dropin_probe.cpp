@@ -320,7 +320,8 @@ int run(int argc, char** argv)
         std::cout << "average " << r.average_us << " tasks " << r.task_count << " samples "
                   << r.timed_samples_us.size() << " capacity " << r.capacity << " schedule "
                   << r.schedule[0] << ',' << r.schedule[1] << ',' << r.schedule[2] << ','
-                  << r.schedule[3] << " hints " << r.cache_hint_bytes << "\n";
+                  << r.schedule[3] << " hints " << r.cache_hint_bytes << " occupancy "
+                  << r.waves_per_simd << "\n";
         write_dense(argv[11], r.output);
     } else if (cmd == "load") {
         need(2);

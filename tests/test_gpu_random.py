@@ -1,6 +1,6 @@
 """Seeded random cross-product of graph family, K, S, costs and launch
 schedule (run length, feature slices, run order, XCD placement, cache hints,
-flags, feature-view alignment) against the oracle.
+occupancy variant, flags, feature-view alignment) against the oracle.
 
 The structured tests in test_gpu_spmm.py cover each setting on fixed graphs;
 these cases draw combinations that no structured test names, with the same
@@ -42,6 +42,7 @@ def draw_case(i):
         "hot_rows": [0, 0, 16, 256, 4096][int(r.integers(5))],
         "flags": [0, 0, 0, capi.ZERO_OUTPUT, capi.PER_TASK][int(r.integers(5))],
         "h_offset": [0, 0, 0, 1, 2][int(r.integers(5))],  # floats past the allocation start
+        "occupancy": [0, 0, 6][int(r.integers(3))],
     }
 
 
@@ -70,6 +71,7 @@ def test_random_schedule_case(gpu_ctx, i):
     gpu_ctx.set_schedule(c["M"], c["SL"])
     gpu_ctx.set_locality(c["order"], c["xcd"])
     gpu_ctx.set_cache_hints(c["hot_rows"] * 4 * K)
+    gpu_ctx.set_occupancy(c["occupancy"])
     try:
         gpu_ctx.spmm(d_rp, d_ci, d_v, d_o, g.n, g.nnz, d_H, g.n, K, d_t, len(p.tasks), C,
                      flags=c["flags"], large_k=large_k)
@@ -78,6 +80,7 @@ def test_random_schedule_case(gpu_ctx, i):
         gpu_ctx.set_schedule(0, 0)
         gpu_ctx.set_locality(0, 0)
         gpu_ctx.set_cache_hints(0)
+        gpu_ctx.set_occupancy(0)
 
     ref = oracle.spmm_mean_f32(p.row_ptr, p.col_idx, p.val, p.origin, H, p.tasks)
     np.testing.assert_allclose(C.cpu().numpy(), ref, rtol=RTOL, atol=ATOL, err_msg=str(c))
@@ -100,3 +103,7 @@ def test_random_schedule_case(gpu_ctx, i):
     expect_vec = 4 if K % 4 == 0 and c["h_offset"] % 4 == 0 else (
         2 if K % 2 == 0 and c["h_offset"] % 2 == 0 else 1)
     assert info["vector_width"] == expect_vec, info
+    f4 = K // info["feature_slices"] // 4
+    o6 = (c["occupancy"] == 6 and not per_task and expect_vec == 4
+          and K % (4 * info["feature_slices"]) == 0 and 2 < f4 <= 16)
+    assert info["waves_per_simd"] == (6 if o6 else 0), (info, c)

@@ -50,30 +50,36 @@ def run_gpu(ctx, p, H, flags=0, c_fill=float("nan"), large_k=False, h_dev=None):
     return C[:p.n, :K].cpu().numpy(), t
 
 
-# (tasks_per_wave, feature_slices, flags, run_order, xcd_blocks, hot_bytes):
-# automatic, the reference's one task per wave, forced task-run fusion / XCD
-# feature slicing (small graphs do not trigger them automatically), runs
-# sorted by output row, contiguous XCD stretches, and cache hints (hot sets
-# of 64 KB / 256 KB of feature rows: a few hundred hot columns, the rest
-# cold, on these small graphs).
-SCHEDULES = [(0, 0, 0, 0, 0, 0), (0, 0, capi.PER_TASK, 0, 0, 0), (3, 1, 0, 1, 1, 0),
-             (8, 2, 0, 1, 1, 0), (16, 4, 0, 1, 1, 0), (64, 4, 0, 1, 1, 0), (2, 1, 0, 2, 1, 0),
-             (5, 1, 0, 1, 2, 0), (8, 4, 0, 2, 2, 0), (1, 2, 0, 2, 2, 0), (0, 0, 0, 0, 0, 1 << 16),
-             (8, 2, 0, 1, 1, 1 << 18), (2, 1, 0, 2, 2, 1 << 16), (0, 0, capi.PER_TASK, 0, 0, 1 << 16)]
+# (tasks_per_wave, feature_slices, flags, run_order, xcd_blocks, hot_bytes,
+# waves_per_simd): automatic, the reference's one task per wave, forced
+# task-run fusion / XCD feature slicing (small graphs do not trigger them
+# automatically), runs sorted by output row, contiguous XCD stretches, cache
+# hints (hot sets of 64 KB / 256 KB of feature rows: a few hundred hot
+# columns, the rest cold, on these small graphs) and the 6-waves-per-SIMD
+# kernel variant (it applies where a feature slice has 9 to 64 floats).
+SCHEDULES = [(0, 0, 0, 0, 0, 0, 0), (0, 0, capi.PER_TASK, 0, 0, 0, 0), (3, 1, 0, 1, 1, 0, 0),
+             (8, 2, 0, 1, 1, 0, 0), (16, 4, 0, 1, 1, 0, 0), (64, 4, 0, 1, 1, 0, 0),
+             (2, 1, 0, 2, 1, 0, 0), (5, 1, 0, 1, 2, 0, 0), (8, 4, 0, 2, 2, 0, 0),
+             (1, 2, 0, 2, 2, 0, 0), (0, 0, 0, 0, 0, 1 << 16, 0), (8, 2, 0, 1, 1, 1 << 18, 0),
+             (2, 1, 0, 2, 2, 1 << 16, 0), (0, 0, capi.PER_TASK, 0, 0, 1 << 16, 0),
+             (0, 0, 0, 0, 0, 0, 6), (3, 2, 0, 2, 2, 0, 6), (8, 1, 0, 1, 1, 1 << 16, 6)]
 SCHED_IDS = ["auto", "per_task", "m3", "m8s2", "m16s4", "m64s4", "m2ord", "m5xcd", "m8s4ordxcd",
-             "m1s2ordxcd", "hints64k", "m8s2_hints256k", "m2ordxcd_hints64k", "per_task_hints"]
+             "m1s2ordxcd", "hints64k", "m8s2_hints256k", "m2ordxcd_hints64k", "per_task_hints",
+             "occ6", "m3s2ordxcd_occ6", "m8_hints64k_occ6"]
 
 
 @pytest.fixture(params=SCHEDULES, ids=SCHED_IDS)
 def sched(request, gpu_ctx):
-    m, sl, flags, order, xcd, hot = request.param
+    m, sl, flags, order, xcd, hot, occ = request.param
     gpu_ctx.set_schedule(m, sl)
     gpu_ctx.set_locality(order, xcd)
     gpu_ctx.set_cache_hints(hot)
+    gpu_ctx.set_occupancy(occ)
     yield flags
     gpu_ctx.set_schedule(0, 0)
     gpu_ctx.set_locality(0, 0)
     gpu_ctx.set_cache_hints(0)
+    gpu_ctx.set_occupancy(0)
 
 
 def check(got, ref):
@@ -774,8 +780,15 @@ def test_schedule_and_locality_arguments(gpu_ctx):
         with pytest.raises(capi.CwlbError) as e:
             gpu_ctx.set_locality(*bad)
         assert e.value.status == capi.INVALID_ARG
+    for bad in (-1, 1, 5, 7, 8):
+        with pytest.raises(capi.CwlbError) as e:
+            gpu_ctx.set_occupancy(bad)
+        assert e.value.status == capi.INVALID_ARG
+    gpu_ctx.set_occupancy(6)
+    assert gpu_ctx.occupancy() == 6
     gpu_ctx.set_schedule(0, 0)
     gpu_ctx.set_locality(0, 0)
+    gpu_ctx.set_occupancy(0)
 
 
 @pytest.mark.parametrize("cfg", [4, 5])
@@ -797,21 +810,25 @@ def test_full_config_locality_modes_agree(gpu_ctx, cfg):
     gpu_ctx.spmm(d_rp, d_ci, d_v, d_o, g.n, g.nnz, H, g.n, K, d_t, len(p.tasks), C0)
     C1 = torch.full_like(C0, float("nan"))
     try:
-        for m, order, xcd, hot in ((4, 2, 1, 0), (8, 2, 2, 0), (32, 1, 2, 0), (64, 1, 1, 48 << 20),
-                                   (8, 2, 2, 96 << 20)):
+        for m, order, xcd, hot, occ in ((4, 2, 1, 0, 0), (8, 2, 2, 0, 0), (32, 1, 2, 0, 0),
+                                        (64, 1, 1, 48 << 20, 0), (8, 2, 2, 96 << 20, 0),
+                                        (2, 2, 2, 0, 6), (64, 1, 1, 48 << 20, 6)):
             gpu_ctx.set_schedule(m, 0)
             gpu_ctx.set_locality(order, xcd)
             gpu_ctx.set_cache_hints(hot)
+            gpu_ctx.set_occupancy(occ)
             C1.fill_(float("nan"))
             gpu_ctx.spmm(d_rp, d_ci, d_v, d_o, g.n, g.nnz, H, g.n, K, d_t, len(p.tasks), C1)
             diff = (C1 - C0).abs()
             bound = RTOL * C0.abs() + ATOL
             assert not torch.isnan(C1).any().item()
-            assert bool((diff <= bound).all().item()), (m, order, xcd, hot, diff.max().item())
+            assert bool((diff <= bound).all().item()), (m, order, xcd, hot, occ,
+                                                        diff.max().item())
     finally:
         gpu_ctx.set_schedule(0, 0)
         gpu_ctx.set_locality(0, 0)
         gpu_ctx.set_cache_hints(0)
+        gpu_ctx.set_occupancy(0)
 
 
 def test_async_call_reports_bad_column_at_synchronize(gpu_ctx):
@@ -927,9 +944,10 @@ def test_tune_schedule(gpu_ctx):
     try:
         m, sl, loc = gpu_ctx.tune_schedule(d_rp, d_ci, d_v, d_o, g.n, g.nnz, d_H, g.n, K, d_t,
                                            len(p.tasks), C, trials=2, locality=True)
-        assert (m, sl) == (0, 0) or (m in (2, 4, 8, 16, 32, 64) and sl in (1, 2, 4))
+        assert (m, sl) == (0, 0) or (m in (1, 2, 4, 8, 16, 32, 64) and sl in (1, 2, 4))
         assert loc in ((0, 0), (2, 1), (2, 2))
         assert gpu_ctx.cache_hints() in (0, 24 << 20, 48 << 20, 96 << 20)
+        assert gpu_ctx.occupancy() in (0, 6)
         ref32, ref64 = oracle_pair(p, g, H)
         check(C.cpu().numpy(), ref32)
         C.fill_(float("nan"))
@@ -941,6 +959,7 @@ def test_tune_schedule(gpu_ctx):
         assert (info["feature_slices"] == sl) if sl else True, info
         assert (info["tasks_per_wave"] == m) if m else True, info
         assert info["run_order"] == (2 if loc[0] == 2 else 1), info
+        assert info["waves_per_simd"] == gpu_ctx.occupancy(), info
         with pytest.raises(capi.CwlbError) as e:
             gpu_ctx.tune_schedule(d_rp, d_ci, d_v, d_o, g.n, g.nnz, d_H, g.n, K, d_t,
                                   len(p.tasks), C, trials=0)
@@ -949,6 +968,7 @@ def test_tune_schedule(gpu_ctx):
         gpu_ctx.set_schedule(0, 0)
         gpu_ctx.set_locality(0, 0)
         gpu_ctx.set_cache_hints(0)
+        gpu_ctx.set_occupancy(0)
 
 
 def test_run_order_reused_across_task_lists(gpu_ctx):
