@@ -233,28 +233,55 @@ def main():
                                  trials=3, locality=True)
 
     # S: the best of the three wave-based candidates (main.cpp:534-577), or fixed.
+    # S: the best of the three wave-based candidates (main.cpp:534-577), or
+    # fixed.  As in the drop-in driver's candidate search (run_single_s per
+    # S), each S gets its launch schedule tuned once (cwlb_ctx_tune_schedule,
+    # outside the timed region), and the S with the fastest tuned aggregation
+    # is kept.  A fixed schedule (--tasks-per-wave etc.) or --no-tune ranks
+    # the S by the automatic schedule instead.
+    fixed = bool(args.tasks_per_wave or args.slices or args.run_order or args.xcd_blocks
+                 or args.hot_mb or args.occupancy)
+    tuning = not fixed and not args.no_tune
     cands = [args.s] if args.s else workloads.candidate_s(g.nnz, info.compute_units)
     best = None
+    s_candidates = []
+    t_tune = 0.0
     for S in cands:
         tk = tasks_for(S)
         d_t = dev(tk.reshape(-1))
+        ctx.set_schedule(0, 0)
+        ctx.set_locality(0, 0)
+        ctx.set_cache_hints(0)
+        ctx.set_occupancy(0)
         for _ in range(5):
             call(d_t, len(tk), False)
-        us = np.mean([call(d_t, len(tk), True).total_us for _ in range(10)])
-        log(f"candidate S={S}: tasks={len(tk)} mean {us:.1f} us")
-        if best is None or us < best[1]:
-            best = (S, us, tk, d_t)
-    S, auto_us, tasks, d_t = best
+        us = float(np.mean([call(d_t, len(tk), True).total_us for _ in range(10)]))
+        rec = {"S": S, "tasks": int(len(tk)), "automatic_us": round(us, 1)}
+        rank = us
+        if tuning:
+            t0 = time.perf_counter()
+            m, sl, (order, xcd) = tune(d_t, len(tk))
+            t_tune += time.perf_counter() - t0
+            rec["schedule"] = {"tasks_per_wave": m, "feature_slices": sl, "run_order": order,
+                               "xcd_blocks": xcd, "hot_bytes": ctx.cache_hints(),
+                               "occupancy": ctx.occupancy()}
+            for _ in range(3):
+                call(d_t, len(tk), False)
+            rank = float(np.mean([call(d_t, len(tk), True).total_us for _ in range(10)]))
+            rec["tuned_us"] = round(rank, 1)
+        log(f"candidate S={S}: {rec}")
+        s_candidates.append(rec)
+        if best is None or rank < best[1]:
+            best = (S, rank, tk, d_t, us, rec.get("schedule"))
+    S, _, tasks, d_t, auto_us, tuned = best
     T = len(tasks)
     prep = preprocessing_times(ctx, g, rp, costs, S, tasks, reorder_host_ms)
     prep["tasks_match_reference_fixture"] = reference_partition_match(cfg, S, costs, tasks)
     log(f"preprocessing: {prep}")
-    # Launch schedule for this graph and S: measured once, like the S search
-    # (cwlb_ctx_tune_schedule; 0, 0 = the automatic choice won).
+    # Launch schedule for this graph and S (0, 0 = the automatic choice).
     schedule = {"tasks_per_wave": 0, "feature_slices": 0, "tuned": False,
                 "automatic_schedule_us": round(float(auto_us), 1)}
-    if (args.tasks_per_wave or args.slices or args.run_order or args.xcd_blocks or args.hot_mb
-            or args.occupancy):
+    if fixed:
         ctx.set_schedule(args.tasks_per_wave, args.slices)
         ctx.set_locality(args.run_order, args.xcd_blocks)
         ctx.set_cache_hints(args.hot_mb << 20)
@@ -263,13 +290,18 @@ def main():
                         run_order=args.run_order, xcd_blocks=args.xcd_blocks,
                         hot_bytes=args.hot_mb << 20, occupancy=args.occupancy)
         log(f"fixed schedule: {schedule}")
-    elif not args.no_tune:
-        t0 = time.perf_counter()
-        m, sl, (order, xcd) = tune(d_t, T)
-        schedule.update(tasks_per_wave=m, feature_slices=sl, run_order=order, xcd_blocks=xcd,
-                        hot_bytes=ctx.cache_hints(), occupancy=ctx.occupancy(), tuned=True,
-                        tuning_ms=round((time.perf_counter() - t0) * 1e3, 1))
+    elif tuning:
+        ctx.set_schedule(tuned["tasks_per_wave"], tuned["feature_slices"])
+        ctx.set_locality(tuned["run_order"], tuned["xcd_blocks"])
+        ctx.set_cache_hints(tuned["hot_bytes"])
+        ctx.set_occupancy(tuned["occupancy"])
+        schedule.update(tuned, tuned=True, tuning_ms=round(t_tune * 1e3, 1))
         log(f"tuned schedule: {schedule}")
+    else:
+        ctx.set_schedule(0, 0)
+        ctx.set_locality(0, 0)
+        ctx.set_cache_hints(0)
+        ctx.set_occupancy(0)
 
     # Timed region: W warm-ups, K steps, synchronised on both sides.
     for _ in range(args.warmup):
@@ -381,6 +413,7 @@ def main():
                    "host_pointer_call_ms": None if host_call_ms is None else round(host_call_ms, 1),
                    "preprocessing": prep,
                    "schedule": schedule,
+                   "s_candidates": s_candidates,
                    **({"s_sweep": s_sweep} if s_sweep else {}),
                    "algorithmic_bytes": b_alg,
                    # measured HBM-side traffic per launch / the same launch time
