@@ -46,14 +46,15 @@ def log(msg):
 
 def measured_traffic(cfg, S):
     """HBM bytes per aggregation launch from the committed rocprofv3 PMC
-    summary: the figure measured at segment size S when the summary has one
-    ("traffic_bytes_per_launch[S=63]: ..."), else its unqualified figure."""
+    summary: the figure measured at segment size S
+    ("traffic_bytes_per_launch[S=63]: ..."), or None when the summary has no
+    figure for this S."""
     try:
         text = open(PMC_SUMMARY[cfg]).read()
     except (KeyError, OSError):
         return None
     found = dict(re.findall(r"traffic_bytes_per_launch(?:\[S=(\d+)\])?:\s*([0-9.eE+]+)", text))
-    value = found.get(str(S), found.get(""))
+    value = found.get(str(S))
     return float(value) if value is not None else None
 
 
