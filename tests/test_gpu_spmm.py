@@ -771,6 +771,27 @@ def test_device_features_match_host(gpu_ctx):
         assert np.array_equal(features_rows(np.arange(rows), K, 42), synth.features(rows, K, 42))
 
 
+def test_fresh_context_defaults_and_last_launch(gpu_ctx):
+    """A new context starts with no cache hints, the standard kernel and an
+    all-zero launch record; after a call the record names the launch."""
+    torch = torch_mod()
+    ctx = capi.Context(0, torch.cuda.current_stream().cuda_stream)
+    try:
+        assert ctx.cache_hints() == 0 and ctx.occupancy() == 0
+        assert all(v == 0 for v in ctx.last_launch().values())
+        g = workloads.small(1, seed=5)
+        p = problem(g, UNIT_COSTS, 8)
+        H = synth.features(g.n, 32, 1)
+        got, _ = run_gpu(ctx, p, H)
+        check(got, oracle.spmm_mean_f32(p.row_ptr, p.col_idx, p.val, p.origin, H, p.tasks))
+        info = ctx.last_launch()
+        assert info["grid_blocks"] > 0 and info["tasks_per_wave"] >= 1, info
+        assert (info["vector_width"], info["run_order"], info["cache_hints"],
+                info["waves_per_simd"]) == (4, 1, 0, 0), info
+    finally:
+        ctx.close()
+
+
 def test_schedule_and_locality_arguments(gpu_ctx):
     for bad in ((-1, 0), (0, 3), (0, 16)):
         with pytest.raises(capi.CwlbError) as e:
