@@ -519,7 +519,9 @@ cwlb_status cwlb_ctx_tune_schedule(cwlb_ctx* ctx, const int32_t* row_ptr, const 
         if (st == CWLB_OK) {
             ctx->sched_occupancy = 6;
             float med = 0.0f;
-            st = time_current(&med, [](const cwlb_ctx* c) { return c->last_launch.waves_per_simd == 6; });
+            st = time_current(&med, [](const cwlb_ctx* c) {
+                return c->last_launch.waves_per_simd == 6;
+            });
             if (st == CWLB_OK && !(med > 0.0f && med < base)) ctx->sched_occupancy = 0;
             if (st == CWLB_OK && ctx->sched_occupancy == 6) {
                 // More waves in flight can move the best run length: its

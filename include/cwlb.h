@@ -242,9 +242,10 @@ cwlb_status cwlb_spmm_mean_f32_large_k(cwlb_ctx* ctx, const int32_t* row_ptr,
  * written there (1, 0 or the context's previous setting = task order kept);
  * then with the occupancy variant (cwlb_ctx_set_occupancy, kept when
  * faster, and then also timed at half and double the run length, so the
- * tasks per wave returned can be 1); then with cache hints of 24, 48 and 96 MB (cwlb_ctx_set_cache_hints), the
- * fastest kept on the context (0 = none; read it with
- * cwlb_ctx_get_cache_hints).  In that mode every timing before the hint
+ * tasks per wave returned can be 1); then with cache hints of 24, 48 and
+ * 96 MB (cwlb_ctx_set_cache_hints), the fastest kept on the context (0 =
+ * none; read it with cwlb_ctx_get_cache_hints); then the standard kernel
+ * again with those hints when the variant was kept.  In that mode every timing before the hint
  * sizes runs without hints, and every timing before the occupancy variant
  * with the standard kernel, whatever the context held.  C receives the
  * result.  Synchronises.  No counterpart in the reference, whose one task
