@@ -56,6 +56,8 @@ cwlb_status read_status(cwlb_ctx* ctx)
     CWLB_HIP_TRY(hipStreamSynchronize(ctx->stream));
     if (st & 1) return fail(CWLB_INVALID_ARG, "spmm: a column index is outside [0, h_rows)");
     if (st & 2) return fail(CWLB_INVALID_ARG, "spmm: an origin entry is outside [0, n_rows)");
+    if (st & 4)
+        return fail(CWLB_INVALID_ARG, "spmm: a row's offsets leave [0, nnz] or decrease (row_ptr)");
     return CWLB_OK;
 }
 
@@ -213,6 +215,32 @@ struct Stager {
     }
 };
 
+// Whether the tasks tile the nonzeros in order: every task well formed and
+// each starting exactly where the previous one ended (the rule by which the
+// aggregation kernel merges consecutive tasks).  Such a list covers each
+// nonzero at most once.
+bool tasks_tile(const cwlb_task* t, int64_t n, int32_t n_rows)
+{
+    auto well_formed = [n_rows](const cwlb_task& x) {
+        return x.row_start >= 0 && x.row_start < x.row_end && x.row_end <= n_rows &&
+               x.first_row_offset >= 0 && x.last_row_nnz >= 0 &&
+               (x.row_end - x.row_start > 1 || x.last_row_nnz == 0 ||
+                x.first_row_offset < x.last_row_nnz);
+    };
+    for (int64_t i = 0; i < n; ++i) {
+        if (!well_formed(t[i])) return false;
+        if (i == 0) continue;
+        const cwlb_task& a = t[i - 1];
+        const cwlb_task& b = t[i];
+        const bool cont = a.last_row_nnz == 0
+                              ? (b.row_start == a.row_end && b.first_row_offset == 0)
+                              : (b.row_start == a.row_end - 1 &&
+                                 b.first_row_offset == a.last_row_nnz);
+        if (!cont) return false;
+    }
+    return true;
+}
+
 template <class T>
 struct DevBuf {
     T* p = nullptr;
@@ -286,6 +314,7 @@ cwlb_status cwlb_ctx_destroy(cwlb_ctx* ctx)
                     static_cast<void*>(ctx->d_col_counts), static_cast<void*>(ctx->d_count_hist),
                     static_cast<void*>(ctx->d_hints)})
         if (p) (void)hipFree(p);
+    for (void* p : ctx->retired) (void)hipFree(p);
     for (int b = 0; b < 2; ++b) {
         if (ctx->stage_ev[b]) (void)hipEventSynchronize(ctx->stage_ev[b]);
         if (ctx->stage_ev[b]) (void)hipEventDestroy(ctx->stage_ev[b]);
@@ -662,7 +691,11 @@ cwlb_status cwlb_spmm_mean_f32_host(cwlb_ctx* ctx, const int32_t* row_ptr,
     }
     SpmmArgs a{d_rp.p, d_ci.p, d_val.p, d_or.p, n_rows, nnz, d_H.p, h_rows, K, d_t.p, n_tasks, d_C.p};
     cwlb_timing local{};
-    s = run_spmm(ctx, a, CWLB_SPMM_ZERO_OUTPUT, &local);
+    // A list that does not tile in order may cover a nonzero twice; one
+    // task per wave then keeps the reference's task-at-a-time result.
+    const uint32_t flags =
+        CWLB_SPMM_ZERO_OUTPUT | (tasks_tile(tasks, n_tasks, n_rows) ? 0u : CWLB_SPMM_PER_TASK);
+    s = run_spmm(ctx, a, flags, &local);
     if (s == CWLB_OK) s = io.to_host(C, d_C.p, sizeof(float) * out_elems);
     if (s != CWLB_OK) {
         (void)hipStreamSynchronize(st);

@@ -123,10 +123,18 @@ cwlb_status build_cache_hints(cwlb_ctx* ctx, const SpmmArgs& a, long long hot_ro
     if (ctx->hint_col == a.col_idx && ctx->hint_nnz == a.nnz && ctx->hint_h_rows == a.h_rows &&
         ctx->hint_hot_rows == hot_rows) {
         *hints = ctx->hint_any_cold ? ctx->d_hints : nullptr;
+        if (!may_build && *hints) ctx->hints_captured = true;
         return CWLB_OK;
     }
     if (!may_build) return CWLB_OK;
     ctx->hint_col = nullptr;  // invalid until rebuilt
+    if (ctx->hints_captured) {
+        // A captured graph reads these bits: keep them until cwlb_ctx_destroy.
+        if (ctx->d_hints) ctx->retired.push_back(ctx->d_hints);
+        ctx->d_hints = nullptr;
+        ctx->hint_cap = 0;
+        ctx->hints_captured = false;
+    }
     hipStream_t st = ctx->stream;
     const long long words = (static_cast<long long>(a.nnz) + 63) / 64;
     long long hist_cap = ctx->d_count_hist ? kBuckets : 0;

@@ -5,6 +5,7 @@
 
 #include <cstdint>
 #include <string>
+#include <vector>
 
 #include "cwlb.h"
 
@@ -20,7 +21,8 @@ struct cwlb_ctx {
     char name[256] = {0};
     char arch[64] = {0};
     // Device status word written by the kernels: bit 0 = a column index was
-    // outside [0, h_rows), bit 1 = an origin entry was outside [0, n_rows).
+    // outside [0, h_rows), bit 1 = an origin entry was outside [0, n_rows),
+    // bit 2 = a row's offsets left [0, nnz] or decreased.
     int* d_status = nullptr;
     // Schedule overrides (0 = automatic): tasks per wave, feature slices,
     // run order (1 = task order, 2 = by output row id) and block placement
@@ -46,6 +48,13 @@ struct cwlb_ctx {
     int order_M = 0;
     void* d_sort_temp = nullptr;
     size_t sort_temp_bytes = 0;
+    // Set when a launch under graph capture used d_run_order (resp.
+    // d_hints): the graph keeps that address, so a later rebuild moves the
+    // buffer to `retired` (freed by cwlb_ctx_destroy) and builds into a new
+    // one instead of rewriting or freeing it.
+    bool order_captured = false;
+    bool hints_captured = false;
+    std::vector<void*> retired;
     // Cache-policy hints of the feature-row gathers (0 = off): the hot set
     // in bytes of feature rows, the per-column in-degrees, their histogram
     // and the per-nonzero cold bits, with what they were built for.

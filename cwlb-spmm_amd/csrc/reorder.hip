@@ -214,6 +214,7 @@ cwlb_status build_run_order(cwlb_ctx* ctx, const SpmmArgs& a, int M, long long n
     if (ctx->order_tasks == a.tasks && ctx->order_origin == a.origin &&
         ctx->order_n_tasks == a.n_tasks && ctx->order_runs == n_runs && ctx->order_M == M) {
         *order = ctx->d_run_order;
+        if (!may_build) ctx->order_captured = true;
         return CWLB_OK;
     }
     if (!may_build) {
@@ -221,6 +222,13 @@ cwlb_status build_run_order(cwlb_ctx* ctx, const SpmmArgs& a, int M, long long n
         return CWLB_OK;
     }
     ctx->order_runs = -1;
+    if (ctx->order_captured) {
+        // A captured graph reads this order: keep it until cwlb_ctx_destroy.
+        if (ctx->d_run_order) ctx->retired.push_back(ctx->d_run_order);
+        ctx->d_run_order = nullptr;
+        ctx->run_cap = 0;
+        ctx->order_captured = false;
+    }
     if (n_runs > ctx->run_cap) {
         cwlb_status s = grow(&ctx->d_run_keys, 0, n_runs);
         if (s == CWLB_OK) s = grow(&ctx->d_run_keys_sorted, 0, n_runs);

@@ -11,12 +11,16 @@
 //
 // Mapping to CDNA4 (64-lane waves):
 //   * a wave executes a run of M consecutive tasks (M = 1 reproduces the
-//     reference's one task per work-group).  Consecutive tasks tile the
-//     nonzeros contiguously, so a run is itself the task
-//     (row_start of its first task, row_end of its last, first_row_offset of
-//     its first, last_row_nnz of its last); a row split only between tasks
-//     of the same run is reduced in registers and stored instead of being
-//     added atomically segment by segment;
+//     reference's one task per work-group).  Inside the run it executes
+//     "segments": maximal stretches of consecutive tasks in which each task
+//     starts exactly where the previous one ended.  A segment is itself a
+//     task (row_start and first_row_offset of its first task, row_end and
+//     last_row_nnz of its last), so a row split only between tasks of one
+//     segment is reduced in registers and stored instead of being added
+//     atomically chunk by chunk.  The partition's task lists tile the
+//     nonzeros in order, so there a segment is the whole run (or a 64-task
+//     window of it); a shuffled list, one with gaps or malformed tasks
+//     falls apart into one-task segments, the reference's semantics;
 //   * a row slice of Ks = K / SL floats is covered by a "slot" of G lanes,
 //     each lane holding R vectors of VEC floats (128-bit loads when
 //     K % 4 == 0); a wave has NS = 64 / G slots.  With SL > 1 the feature
@@ -37,8 +41,9 @@
 //     range (up to 256 nonzeros) at once, into a per-wave LDS window, so no
 //     row waits on an index load before its feature-row loads.  C is written
 //     with streaming stores.
-// Split rows are cleared by zero_first_segments before the main kernel, by
-// the run that owns their first segment, so each is cleared exactly once.
+// Split rows are cleared by zero_split_rows before the main kernel: a row
+// that a segment leaves open is cleared by the task whose chunk of it starts
+// at nonzero 0.
 #include "internal.h"
 
 #include <algorithm>
@@ -201,14 +206,14 @@ __device__ __forceinline__ int wave_max(int v)
 }
 
 // Nonzero range of row r inside task (rs, re, fo, ln), with the reference's
-// clamps (parallelMatrix.cpp:164-176).  Rows with deg <= 0 have an empty
-// chunk.  A row whose offsets leave [0, nnz) gets an empty chunk too, so no
-// load can leave the arrays.
+// clamps (parallelMatrix.cpp:164-176).  Rows of degree 0 have an empty
+// chunk.  A row whose offsets leave [0, nnz] or decrease gets d = -1 and an
+// empty chunk: no load can leave the arrays, and the caller reports it.
 struct Chunk {
     int base;  // row_ptr[r]
     int b;     // chunk begin within the row
     int e;     // chunk end within the row
-    int d;     // full degree
+    int d;     // full degree (-1: malformed offsets)
 };
 
 __device__ __forceinline__ Chunk row_chunk(const int* __restrict__ rp, int r, int rs, int re,
@@ -218,10 +223,14 @@ __device__ __forceinline__ Chunk row_chunk(const int* __restrict__ rp, int r, in
     const int p0 = rp[r];
     const int p1 = rp[r + 1];
     c.base = p0;
-    c.d = p1 - p0;
     c.b = 0;
     c.e = 0;
-    if (c.d <= 0 || p0 < 0 || static_cast<long long>(p1) > nnz) return c;
+    if (p0 < 0 || p1 < p0 || static_cast<long long>(p1) > nnz) {
+        c.d = -1;
+        return c;
+    }
+    c.d = p1 - p0;
+    if (c.d == 0) return c;
     int b = (r == rs) ? fo : 0;
     int e = c.d;
     if (r == re - 1 && ln > 0) e = ln;
@@ -244,29 +253,48 @@ __device__ __forceinline__ int fresh(int x)
     return x;
 }
 
-// Bounds of run `run` (tasks [run*M, min(run*M + M, n_tasks))) as one task.
-struct RunTask {
-    int rs, re, fo, ln;
-};
-
-__device__ __forceinline__ RunTask run_task(const cwlb_task* __restrict__ tasks,
-                                            long long n_tasks, long long run, int M)
+// ------------------------------------------------------------ segments
+// A task is well formed when its rows lie in [0, n_rows), it has at least
+// one row, its offsets are non-negative, and a one-row task with an end
+// offset ends after it starts.
+__device__ __forceinline__ bool task_well_formed(const cwlb_task& t, int n_rows)
 {
-    const long long t0 = run * M;
-    const long long tl = (t0 + M <= n_tasks ? t0 + M : n_tasks) - 1;
-    const cwlb_task a = tasks[t0];
-    RunTask r;
-    r.rs = a.row_start;
-    r.fo = a.first_row_offset;
-    if (tl == t0) {
-        r.re = a.row_end;
-        r.ln = a.last_row_nnz;
-    } else {
-        const cwlb_task z = tasks[tl];
-        r.re = z.row_end;
-        r.ln = z.last_row_nnz;
-    }
-    return r;
+    return t.row_start >= 0 && t.row_start < t.row_end && t.row_end <= n_rows &&
+           t.first_row_offset >= 0 && t.last_row_nnz >= 0 &&
+           (t.row_end - t.row_start > 1 || t.last_row_nnz == 0 ||
+            t.first_row_offset < t.last_row_nnz);
+}
+
+// b starts exactly where a ends: on the row after a's last row when a ends
+// on a row boundary (last_row_nnz == 0), else inside a's last row at a's
+// end offset.
+__device__ __forceinline__ bool continues(const cwlb_task& a, const cwlb_task& b)
+{
+    return a.last_row_nnz == 0
+               ? (b.row_start == a.row_end && b.first_row_offset == 0)
+               : (b.row_start == a.row_end - 1 && b.first_row_offset == a.last_row_nnz);
+}
+
+// Whether task cur, at position in_run inside its run of M tasks (prev is
+// the task before it), starts a segment: at every 64-task window of a run
+// (the run's first task included), and wherever either task is malformed or
+// cur does not continue prev.  The aggregation kernel and the split-row
+// clearing pass use this same rule.
+__device__ __forceinline__ bool segment_break(const cwlb_task& prev, const cwlb_task& cur,
+                                              long long in_run, int n_rows)
+{
+    return (in_run & 63) == 0 || !task_well_formed(prev, n_rows) ||
+           !task_well_formed(cur, n_rows) || !continues(prev, cur);
+}
+
+__device__ __forceinline__ cwlb_task shfl_up_task(const cwlb_task& t)
+{
+    cwlb_task p;
+    p.row_start = __shfl_up(t.row_start, 1);
+    p.row_end = __shfl_up(t.row_end, 1);
+    p.first_row_offset = __shfl_up(t.first_row_offset, 1);
+    p.last_row_nnz = __shfl_up(t.last_row_nnz, 1);
+    return p;
 }
 
 // Block b runs on XCD b % 8; slice = XCD % SL.  The P = 8 / SL XCDs of one
@@ -333,13 +361,6 @@ spmm_mean_runs(const int* __restrict__ rp, const int* __restrict__ ci,
     // that order instead of task order.
     const long long run = run_order ? static_cast<long long>(run_order[pos]) : pos;
 
-    const RunTask tk = run_task(tasks, n_tasks, run, M);
-    const int rs = tk.rs;
-    const int re = tk.re;
-    const int fo = tk.fo;
-    const int ln = tk.ln;
-    const int rlo = max(rs, 0);
-    const int rhi = min(re, n_rows);
     const int K = ld / SL;                       // features of this slice
     const float* __restrict__ Hs = H + slice * K;
     float* __restrict__ Cs = C + slice * K;
@@ -351,257 +372,96 @@ spmm_mean_runs(const int* __restrict__ rp, const int* __restrict__ ci,
     if constexpr (HN) hrsrc = feature_rsrc(H, h_rows, ld);
     const unsigned slice_bytes = static_cast<unsigned>(slice * K) * 4u;
 
-    for (int pass = 0; pass < npass; ++pass) {
-        const int fl = pass * G * R + sub;  // first vector element of this lane
-        int r = rlo;
-        while (r < rhi) {
-            const Chunk c0 = row_chunk(rp, r, rs, re, fo, ln, nnz);
-            const int len0 = c0.e - c0.b;
-            if (len0 >= kLong) {
-                // ---------------- long chunk: all slots on one row
-                V acc[R];
+    // One segment: task (rs, re, fo, ln).
+    auto run_segment = [&](const int rs, const int re, const int fo, const int ln) {
+        const int rlo = max(rs, 0);
+        const int rhi = min(re, n_rows);
+        for (int pass = 0; pass < npass; ++pass) {
+            const int fl = pass * G * R + sub;  // first vector element of this lane
+            int r = rlo;
+            while (r < rhi) {
+                const Chunk c0 = row_chunk(rp, r, rs, re, fo, ln, nnz);
+                const int len0 = c0.e - c0.b;
+                if (len0 >= kLong) {
+                    // ---------------- long chunk: all slots on one row
+                    V acc[R];
 #pragma unroll
-                for (int q = 0; q < R; ++q) acc[q] = vzero<VEC>();
-                for (int w0 = c0.b; w0 < c0.e; w0 += 64) {
-                    const int wn = min(64, c0.e - w0);
-                    const int lane = fresh(threadIdx.x & 63);
-                    int colw = 0;
-                    float valw = 0.0f;
-                    if (lane < wn) {
-                        colw = __builtin_nontemporal_load(ci + c0.base + w0 + lane);
-                        valw = __builtin_nontemporal_load(val + c0.base + w0 + lane);
-                        if constexpr (HN) colw = with_hint(colw, hints, c0.base + w0 + lane);
-                    }
-                    for (int k0 = 0; k0 < wn; k0 += STEP) {
-                        int cc[UL];
-                        float a[UL];
-                        bool ok[UL];
-                        bool cold[UL];
-                        const int sl = fresh(slot);
+                    for (int q = 0; q < R; ++q) acc[q] = vzero<VEC>();
+                    for (int w0 = c0.b; w0 < c0.e; w0 += 64) {
+                        const int wn = min(64, c0.e - w0);
+                        const int lane = fresh(threadIdx.x & 63);
+                        int colw = 0;
+                        float valw = 0.0f;
+                        if (lane < wn) {
+                            colw = __builtin_nontemporal_load(ci + c0.base + w0 + lane);
+                            valw = __builtin_nontemporal_load(val + c0.base + w0 + lane);
+                            if constexpr (HN) colw = with_hint(colw, hints, c0.base + w0 + lane);
+                        }
+                        for (int k0 = 0; k0 < wn; k0 += STEP) {
+                            int cc[UL];
+                            float a[UL];
+                            bool ok[UL];
+                            bool cold[UL];
+                            const int sl = fresh(slot);
 #pragma unroll
-                        for (int u = 0; u < UL; ++u) {
-                            const int jj = k0 + u * NS + sl;
-                            cc[u] = __shfl(colw, jj & 63);
-                            a[u] = __shfl(valw, jj & 63);
-                            cold[u] = HN && cc[u] < 0;
-                            if constexpr (HN) cc[u] &= 0x7fffffff;
-                            ok[u] = jj < wn;
-                            if (ok[u] && static_cast<unsigned long long>(cc[u]) >=
-                                             static_cast<unsigned long long>(h_rows)) {
-                                ok[u] = false;
-                                bad |= 1;
+                            for (int u = 0; u < UL; ++u) {
+                                const int jj = k0 + u * NS + sl;
+                                cc[u] = __shfl(colw, jj & 63);
+                                a[u] = __shfl(valw, jj & 63);
+                                cold[u] = HN && cc[u] < 0;
+                                if constexpr (HN) cc[u] &= 0x7fffffff;
+                                ok[u] = jj < wn;
+                                if (ok[u] && static_cast<unsigned long long>(cc[u]) >=
+                                                 static_cast<unsigned long long>(h_rows)) {
+                                    ok[u] = false;
+                                    bad |= 1;
+                                }
+                            }
+                            V h[UL][R];
+#pragma unroll
+                            for (int u = 0; u < UL; ++u) {
+                                const float* hrow = Hs + static_cast<size_t>(cc[u]) * ld;
+#pragma unroll
+                                for (int q = 0; q < R; ++q) {
+                                    const int f = fl + G * q;
+                                    if constexpr (HN)
+                                        h[u][q] = (ok[u] && f < F)
+                                                      ? gather_hinted(hrsrc,
+                                                                      static_cast<unsigned>(cc[u]) * ld * 4u +
+                                                                          slice_bytes + f * 16u,
+                                                                      cold[u])
+                                                      : vzero<VEC>();
+                                    else
+                                        h[u][q] = (ok[u] && f < F) ? vload<VEC>(hrow + f * VEC)
+                                                                   : vzero<VEC>();
+                                }
+                            }
+#pragma unroll
+                            for (int u = 0; u < UL; ++u) {
+                                if (ok[u]) {
+#pragma unroll
+                                    for (int q = 0; q < R; ++q) acc[q] = vfma(a[u], h[u][q], acc[q]);
+                                }
                             }
                         }
-                        V h[UL][R];
-#pragma unroll
-                        for (int u = 0; u < UL; ++u) {
-                            const float* hrow = Hs + static_cast<size_t>(cc[u]) * ld;
-#pragma unroll
-                            for (int q = 0; q < R; ++q) {
-                                const int f = fl + G * q;
-                                if constexpr (HN)
-                                    h[u][q] = (ok[u] && f < F)
-                                                  ? gather_hinted(hrsrc,
-                                                                  static_cast<unsigned>(cc[u]) * ld * 4u +
-                                                                      slice_bytes + f * 16u,
-                                                                  cold[u])
-                                                  : vzero<VEC>();
-                                else
-                                    h[u][q] = (ok[u] && f < F) ? vload<VEC>(hrow + f * VEC)
-                                                               : vzero<VEC>();
-                            }
-                        }
-#pragma unroll
-                        for (int u = 0; u < UL; ++u) {
-                            if (ok[u]) {
-#pragma unroll
-                                for (int q = 0; q < R; ++q) acc[q] = vfma(a[u], h[u][q], acc[q]);
-                            }
-                        }
                     }
-                }
 #pragma unroll
-                for (int off = G; off < 64; off <<= 1) {
+                    for (int off = G; off < 64; off <<= 1) {
 #pragma unroll
-                    for (int q = 0; q < R; ++q) acc[q] = acc[q] + vshfl_xor(acc[q], off);
-                }
-                const int o = origin[r];
-                if (static_cast<unsigned>(o) >= static_cast<unsigned>(n_rows)) {
-                    bad |= 2;
-                } else if (slot == 0) {
-                    float* crow = Cs + static_cast<size_t>(o) * ld;
-                    const float fd = static_cast<float>(c0.d);
-                    const bool full = (c0.b == 0 && c0.e == c0.d);
-#pragma unroll
-                    for (int q = 0; q < R; ++q) {
-                        const int f = fl + G * q;
-                        if (f < F) {
-                            const V res = vdiv(acc[q], fd);
-                            if (full)
-                                vstore_nt<VEC>(crow + f * VEC, res);
-                            else
-                                vatomic_add(crow + f * VEC, res);
-                        }
+                        for (int q = 0; q < R; ++q) acc[q] = acc[q] + vshfl_xor(acc[q], off);
                     }
-                }
-                ++r;
-                continue;
-            }
-
-            // ---------------- short rows: one row per slot, RU rows per slot
-            const int lane = fresh(threadIdx.x & 63);
-            const int rr = r + lane;
-            const bool mine = lane < GROUP && rr < rhi;
-            Chunk my = {0, 0, 0, 0};
-            if (mine) my = row_chunk(rp, rr, rs, re, fo, ln, nnz);
-            const int mylen = my.e - my.b;
-            // The group: the leading rows that are short, start where the
-            // previous row's chunk ends (always, for a non-decreasing
-            // row_ptr) and end within kWin nonzeros of the group's start.
-            // The first row always qualifies (its chunk is shorter than
-            // kLong <= kWin), so every group makes progress, and the
-            // group's nonzeros are the contiguous range [gs, gs + gn).
-            const int mys = my.base + my.b;
-            const int mye = my.base + my.e;
-            const int gs = c0.base + c0.b;
-            const int prev_end = __shfl_up(mye, 1);
-            const bool fits = mine && mylen < kLong && (lane == 0 || mys == prev_end) &&
-                              mye - gs <= kWin;
-            const unsigned long long stop = __ballot(!fits);
-            int cnt = min(GROUP, rhi - r);
-            if (stop) cnt = min(cnt, static_cast<int>(__ffsll(static_cast<long long>(stop))) - 1);
-            const int myo = (mine && lane < cnt) ? origin[rr] : 0;
-            const int ge = __shfl(mye, cnt - 1);
-            const int gn = (gs >= 0 && static_cast<long long>(ge) <= nnz) ? ge - gs : 0;
-            int colw = 0;
-            float valw = 0.0f;
-            if constexpr (kStage > 0) {
-                // The previous group's reads of this wave's window are done
-                // (wave-ordered LDS); the fences keep the compiler from
-                // moving accesses across the exchange.
-                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-                __builtin_amdgcn_wave_barrier();
-                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-                // All loads first, then the LDS writes: one memory round trip.
-                constexpr int NT = (kStage + 63) / 64;
-                int lc[NT];
-                float lv[NT];
-#pragma unroll
-                for (int t = 0; t < NT; ++t) {
-                    const int i = lane + 64 * t;
-                    lc[t] = i < gn ? __builtin_nontemporal_load(ci + gs + i) : 0;
-                    lv[t] = i < gn ? __builtin_nontemporal_load(val + gs + i) : 0.0f;
-                    if constexpr (HN)
-                        if (i < gn) lc[t] = with_hint(lc[t], hints, gs + i);
-                }
-#pragma unroll
-                for (int t = 0; t < NT; ++t) {
-                    const int i = lane + 64 * t;
-                    if (i < gn) {
-                        wcol[i] = lc[t];
-                        wval[i] = lv[t];
-                    }
-                }
-                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-                __builtin_amdgcn_wave_barrier();
-                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-            } else if (lane < gn) {
-                colw = __builtin_nontemporal_load(ci + gs + lane);
-                valw = __builtin_nontemporal_load(val + gs + lane);
-                if constexpr (HN) colw = with_hint(colw, hints, gs + lane);
-            }
-            V acc[RU][R];
-            int pos[RU];
-            int len[RU];
-            int maxlen = 0;
-#pragma unroll
-            for (int u = 0; u < RU; ++u) {
-                const int gi = u * NS + fresh(slot);
-                pos[u] = __shfl(mys - gs, gi);  // window position of the chunk
-                len[u] = __shfl(mylen, gi);
-                if (gi >= cnt) len[u] = 0;
-                maxlen = max(maxlen, len[u]);
-#pragma unroll
-                for (int q = 0; q < R; ++q) acc[u][q] = vzero<VEC>();
-            }
-            const int jmax = wave_max(maxlen);
-            for (int j = 0; j < jmax; ++j) {
-                int cc[RU];
-                float a[RU];
-                bool ok[RU];
-                bool cold[RU];
-#pragma unroll
-                for (int u = 0; u < RU; ++u) {
-                    ok[u] = j < len[u];
-                    const int src = pos[u] + j;  // in [0, gn) whenever ok[u]
-                    if constexpr (kStage > 0) {
-                        cc[u] = wcol[ok[u] ? src : 0];
-                        a[u] = wval[ok[u] ? src : 0];
-                    } else {
-                        cc[u] = __shfl(colw, src & 63);
-                        a[u] = __shfl(valw, src & 63);
-                    }
-                    cold[u] = HN && cc[u] < 0;
-                    if constexpr (HN) cc[u] &= 0x7fffffff;
-                    if (ok[u] && static_cast<unsigned long long>(cc[u]) >=
-                                     static_cast<unsigned long long>(h_rows)) {
-                        ok[u] = false;
-                        bad |= 1;
-                    }
-                }
-                V h[RU][R];
-#pragma unroll
-                for (int u = 0; u < RU; ++u) {
-                    const float* hrow = Hs + static_cast<size_t>(cc[u]) * ld;
-#pragma unroll
-                    for (int q = 0; q < R; ++q) {
-                        const int f = fl + G * q;
-                        if constexpr (HN)
-                            h[u][q] = (ok[u] && f < F)
-                                          ? gather_hinted(hrsrc,
-                                                          static_cast<unsigned>(cc[u]) * ld * 4u +
-                                                              slice_bytes + f * 16u,
-                                                          cold[u])
-                                          : vzero<VEC>();
-                        else
-                            h[u][q] = (ok[u] && f < F) ? vload<VEC>(hrow + f * VEC) : vzero<VEC>();
-                    }
-                }
-#pragma unroll
-                for (int u = 0; u < RU; ++u) {
-                    if (ok[u]) {
-#pragma unroll
-                        for (int q = 0; q < R; ++q) acc[u][q] = vfma(a[u], h[u][q], acc[u][q]);
-                    }
-                }
-            }
-#pragma unroll
-            for (int u = 0; u < RU; ++u) {
-                const int gi = u * NS + fresh(slot);
-                const int o = __shfl(myo, gi);
-                const int d = __shfl(my.d, gi);
-                const int b = __shfl(my.b, gi);
-                const int e = __shfl(my.e, gi);
-                if (gi < cnt) {
+                    const int o = origin[r];
                     if (static_cast<unsigned>(o) >= static_cast<unsigned>(n_rows)) {
                         bad |= 2;
-                        continue;
-                    }
-                    float* crow = Cs + static_cast<size_t>(o) * ld;
-                    if (d <= 0) {
-#pragma unroll
-                        for (int q = 0; q < R; ++q) {
-                            const int f = fl + G * q;
-                            if (f < F) vstore_nt<VEC>(crow + f * VEC, vzero<VEC>());
-                        }
-                    } else if (e > b) {
-                        const float fd = static_cast<float>(d);
-                        const bool full = (b == 0 && e == d);
+                    } else if (slot == 0) {
+                        float* crow = Cs + static_cast<size_t>(o) * ld;
+                        const float fd = static_cast<float>(c0.d);
+                        const bool full = (c0.b == 0 && c0.e == c0.d);
 #pragma unroll
                         for (int q = 0; q < R; ++q) {
                             const int f = fl + G * q;
                             if (f < F) {
-                                const V res = vdiv(acc[u][q], fd);
+                                const V res = vdiv(acc[q], fd);
                                 if (full)
                                     vstore_nt<VEC>(crow + f * VEC, res);
                                 else
@@ -609,43 +469,271 @@ spmm_mean_runs(const int* __restrict__ rp, const int* __restrict__ ci,
                             }
                         }
                     }
+                    ++r;
+                    continue;
                 }
+
+                // ---------------- short rows: one row per slot, RU rows per slot
+                const int lane = fresh(threadIdx.x & 63);
+                const int rr = r + lane;
+                const bool mine = lane < GROUP && rr < rhi;
+                Chunk my = {0, 0, 0, 0};
+                if (mine) my = row_chunk(rp, rr, rs, re, fo, ln, nnz);
+                const int mylen = my.e - my.b;
+                // The group: the leading rows that are short, start where the
+                // previous row's chunk ends (always, for a non-decreasing
+                // row_ptr) and end within kWin nonzeros of the group's start.
+                // The first row always qualifies (its chunk is shorter than
+                // kLong <= kWin), so every group makes progress, and the
+                // group's nonzeros are the contiguous range [gs, gs + gn).
+                const int mys = my.base + my.b;
+                const int mye = my.base + my.e;
+                const int gs = c0.base + c0.b;
+                const int prev_end = __shfl_up(mye, 1);
+                const bool fits = mine && mylen < kLong && (lane == 0 || mys == prev_end) &&
+                                  mye - gs <= kWin;
+                const unsigned long long stop = __ballot(!fits);
+                int cnt = min(GROUP, rhi - r);
+                if (stop) cnt = min(cnt, static_cast<int>(__ffsll(static_cast<long long>(stop))) - 1);
+                const int myo = (mine && lane < cnt) ? origin[rr] : 0;
+                const int ge = __shfl(mye, cnt - 1);
+                const int gn = (gs >= 0 && static_cast<long long>(ge) <= nnz) ? ge - gs : 0;
+                int colw = 0;
+                float valw = 0.0f;
+                if constexpr (kStage > 0) {
+                    // The previous group's reads of this wave's window are done
+                    // (wave-ordered LDS); the fences keep the compiler from
+                    // moving accesses across the exchange.
+                    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                    __builtin_amdgcn_wave_barrier();
+                    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                    // All loads first, then the LDS writes: one memory round trip.
+                    constexpr int NT = (kStage + 63) / 64;
+                    int lc[NT];
+                    float lv[NT];
+#pragma unroll
+                    for (int t = 0; t < NT; ++t) {
+                        const int i = lane + 64 * t;
+                        lc[t] = i < gn ? __builtin_nontemporal_load(ci + gs + i) : 0;
+                        lv[t] = i < gn ? __builtin_nontemporal_load(val + gs + i) : 0.0f;
+                        if constexpr (HN)
+                            if (i < gn) lc[t] = with_hint(lc[t], hints, gs + i);
+                    }
+#pragma unroll
+                    for (int t = 0; t < NT; ++t) {
+                        const int i = lane + 64 * t;
+                        if (i < gn) {
+                            wcol[i] = lc[t];
+                            wval[i] = lv[t];
+                        }
+                    }
+                    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                    __builtin_amdgcn_wave_barrier();
+                    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                } else if (lane < gn) {
+                    colw = __builtin_nontemporal_load(ci + gs + lane);
+                    valw = __builtin_nontemporal_load(val + gs + lane);
+                    if constexpr (HN) colw = with_hint(colw, hints, gs + lane);
+                }
+                V acc[RU][R];
+                int pos[RU];
+                int len[RU];
+                int maxlen = 0;
+#pragma unroll
+                for (int u = 0; u < RU; ++u) {
+                    const int gi = u * NS + fresh(slot);
+                    pos[u] = __shfl(mys - gs, gi);  // window position of the chunk
+                    len[u] = __shfl(mylen, gi);
+                    if (gi >= cnt) len[u] = 0;
+                    maxlen = max(maxlen, len[u]);
+#pragma unroll
+                    for (int q = 0; q < R; ++q) acc[u][q] = vzero<VEC>();
+                }
+                const int jmax = wave_max(maxlen);
+                for (int j = 0; j < jmax; ++j) {
+                    int cc[RU];
+                    float a[RU];
+                    bool ok[RU];
+                    bool cold[RU];
+#pragma unroll
+                    for (int u = 0; u < RU; ++u) {
+                        ok[u] = j < len[u];
+                        const int src = pos[u] + j;  // in [0, gn) whenever ok[u]
+                        if constexpr (kStage > 0) {
+                            cc[u] = wcol[ok[u] ? src : 0];
+                            a[u] = wval[ok[u] ? src : 0];
+                        } else {
+                            cc[u] = __shfl(colw, src & 63);
+                            a[u] = __shfl(valw, src & 63);
+                        }
+                        cold[u] = HN && cc[u] < 0;
+                        if constexpr (HN) cc[u] &= 0x7fffffff;
+                        if (ok[u] && static_cast<unsigned long long>(cc[u]) >=
+                                         static_cast<unsigned long long>(h_rows)) {
+                            ok[u] = false;
+                            bad |= 1;
+                        }
+                    }
+                    V h[RU][R];
+#pragma unroll
+                    for (int u = 0; u < RU; ++u) {
+                        const float* hrow = Hs + static_cast<size_t>(cc[u]) * ld;
+#pragma unroll
+                        for (int q = 0; q < R; ++q) {
+                            const int f = fl + G * q;
+                            if constexpr (HN)
+                                h[u][q] = (ok[u] && f < F)
+                                              ? gather_hinted(hrsrc,
+                                                              static_cast<unsigned>(cc[u]) * ld * 4u +
+                                                                  slice_bytes + f * 16u,
+                                                              cold[u])
+                                              : vzero<VEC>();
+                            else
+                                h[u][q] = (ok[u] && f < F) ? vload<VEC>(hrow + f * VEC) : vzero<VEC>();
+                        }
+                    }
+#pragma unroll
+                    for (int u = 0; u < RU; ++u) {
+                        if (ok[u]) {
+#pragma unroll
+                            for (int q = 0; q < R; ++q) acc[u][q] = vfma(a[u], h[u][q], acc[u][q]);
+                        }
+                    }
+                }
+#pragma unroll
+                for (int u = 0; u < RU; ++u) {
+                    const int gi = u * NS + fresh(slot);
+                    const int o = __shfl(myo, gi);
+                    const int d = __shfl(my.d, gi);
+                    const int b = __shfl(my.b, gi);
+                    const int e = __shfl(my.e, gi);
+                    if (gi < cnt) {
+                        if (d < 0) {
+                            bad |= 4;
+                            continue;
+                        }
+                        if (static_cast<unsigned>(o) >= static_cast<unsigned>(n_rows)) {
+                            bad |= 2;
+                            continue;
+                        }
+                        float* crow = Cs + static_cast<size_t>(o) * ld;
+                        if (d == 0) {
+#pragma unroll
+                            for (int q = 0; q < R; ++q) {
+                                const int f = fl + G * q;
+                                if (f < F) vstore_nt<VEC>(crow + f * VEC, vzero<VEC>());
+                            }
+                        } else if (e > b) {
+                            const float fd = static_cast<float>(d);
+                            const bool full = (b == 0 && e == d);
+#pragma unroll
+                            for (int q = 0; q < R; ++q) {
+                                const int f = fl + G * q;
+                                if (f < F) {
+                                    const V res = vdiv(acc[u][q], fd);
+                                    if (full)
+                                        vstore_nt<VEC>(crow + f * VEC, res);
+                                    else
+                                        vatomic_add(crow + f * VEC, res);
+                                }
+                            }
+                        }
+                    }
+                }
+                r += cnt;
             }
-            r += cnt;
         }
+    };
+
+    // The run's tasks, 64 at a time: the window's segment starts by ballot
+    // (one coalesced load of the window), then the segments in order, each
+    // reading its first and last task.
+    const long long t0 = run * M;
+    const int cnt = static_cast<int>(min(static_cast<long long>(M), n_tasks - t0));
+    for (int w = 0; w < cnt; w += 64) {
+        const int wn = min(64, cnt - w);
+        const long long tw = t0 + w;
+        unsigned long long rest;
+        {
+            // Lane i compares task i of the window with task i - 1 (both
+            // loaded by the lane itself: a cross-lane shuffle here would keep
+            // a lane-id register alive through the whole kernel).
+            const int lane = fresh(threadIdx.x & 63);
+            bool brk = lane == 0;
+            if (lane > 0 && lane < wn)
+                brk = segment_break(tasks[tw + lane - 1], tasks[tw + lane], w + lane, n_rows);
+            rest = __ballot(lane < wn && brk);
+        }
+        do {
+            const int s0 = __builtin_ctzll(rest);
+            rest &= rest - 1;
+            const int e0 = rest ? __builtin_ctzll(rest) : wn;
+            const cwlb_task a = tasks[tw + s0];
+            const cwlb_task z = tasks[tw + e0 - 1];
+            run_segment(a.row_start, z.row_end, a.first_row_offset, z.last_row_nnz);
+        } while (rest);
     }
     if (bad) atomicOr(status, bad);
 }
 
-// Clears, once each, the C rows that receive atomic partial sums: a row is
-// cleared by the run whose chunk of it starts at nonzero 0 without reaching
-// the row's end (only a run's first and last rows can be partial).  One lane
-// per run; the wave then clears the marked rows with coalesced stores.
-// Block 0 also resets the status word.
+// Clears the C rows that receive atomic partial sums.  One lane per task,
+// with the segment rule of the aggregation kernel: a row whose chunk in a
+// task starts at nonzero 0 and stops before the row's end is left open by
+// that task (only a task's first and last rows can be).  The row is
+// completed inside the segment, and later stored whole, when the following
+// tasks continue it (no segment start in between) up to one whose chunk
+// reaches the row's end; otherwise every segment adds a part of it
+// atomically and it is cleared here.  The scan ahead stops at the wave's
+// last lane: a row it cannot follow further is cleared, which costs only
+// a store when the row is later stored whole.  The wave clears the marked
+// rows with coalesced stores.  Block 0 also resets the status word.
 template <int VEC>
 __global__ void __launch_bounds__(kBlock)
-zero_first_segments(const int* __restrict__ rp, const int* __restrict__ origin, int n_rows,
-                    long long nnz, const cwlb_task* __restrict__ tasks, long long n_tasks, int M,
-                    long long n_runs, int K, float* __restrict__ C, int* __restrict__ status)
+zero_split_rows(const int* __restrict__ rp, const int* __restrict__ origin, int n_rows,
+                long long nnz, const cwlb_task* __restrict__ tasks, long long n_tasks, int M,
+                int K, float* __restrict__ C, int* __restrict__ status)
 {
     const int lane = threadIdx.x & 63;
-    const long long run = static_cast<long long>(blockIdx.x) * kBlock + threadIdx.x;
+    const long long t = static_cast<long long>(blockIdx.x) * kBlock + threadIdx.x;
     if (blockIdx.x == 0 && threadIdx.x == 0) *status = 0;
-    int o1 = -1, o2 = -1;
-    if (run < n_runs) {
-        const RunTask tk = run_task(tasks, n_tasks, run, M);
-        const int rlo = max(tk.rs, 0);
-        const int rhi = min(tk.re, n_rows);
+    cwlb_task cur{0, 0, 0, 0};
+    if (t < n_tasks) cur = tasks[t];
+    cwlb_task prev = shfl_up_task(cur);
+    if (lane == 0 && t > 0 && t < n_tasks) prev = tasks[t - 1];
+    bool brk = true;    // task t starts a segment (lanes past the end count as starts)
+    bool ends = false;  // task t's chunk of its first row reaches that row's end
+    int o1 = -1;        // first row, left open (a task that is not its last row)
+    int o2 = -1;        // last row, left open
+    if (t < n_tasks) {
+        const long long in_run = t % M;
+        brk = segment_break(prev, cur, in_run, n_rows);
+        const int rs = cur.row_start, re = cur.row_end;
+        const int fo = cur.first_row_offset, ln = cur.last_row_nnz;
+        const int rlo = max(rs, 0);
+        const int rhi = min(re, n_rows);
         if (rlo < rhi) {
-            const Chunk a = row_chunk(rp, rlo, tk.rs, tk.re, tk.fo, tk.ln, nnz);
-            if (a.d > 0 && a.b == 0 && a.e > 0 && a.e < a.d) o1 = origin[rlo];
-            if (rhi - 1 != rlo) {
-                const Chunk z = row_chunk(rp, rhi - 1, tk.rs, tk.re, tk.fo, tk.ln, nnz);
+            const Chunk a = row_chunk(rp, rlo, rs, re, fo, ln, nnz);
+            ends = a.e == a.d;
+            const bool open_a = a.d > 0 && a.b == 0 && a.e > 0 && a.e < a.d;
+            if (rhi - 1 == rlo) {
+                if (open_a) o2 = origin[rlo];
+            } else {
+                if (open_a) o1 = origin[rlo];
+                const Chunk z = row_chunk(rp, rhi - 1, rs, re, fo, ln, nnz);
                 if (z.d > 0 && z.b == 0 && z.e > 0 && z.e < z.d) o2 = origin[rhi - 1];
             }
         }
         if (o1 >= n_rows) o1 = -1;
         if (o2 >= n_rows) o2 = -1;
+    }
+    const unsigned long long mb = __ballot(brk);
+    const unsigned long long me = __ballot(ends);
+    if (o2 >= 0 && lane < 63) {
+        const unsigned long long ahead = (mb | me) >> (lane + 1);
+        if (ahead) {
+            const int u = lane + 1 + __builtin_ctzll(ahead);
+            if (!((mb >> u) & 1ull)) o2 = -1;  // completed inside the segment
+        }
     }
     const int F = K / VEC;
     unsigned long long m = __ballot(o1 >= 0);
@@ -666,20 +754,23 @@ zero_first_segments(const int* __restrict__ rp, const int* __restrict__ origin, 
     }
 }
 
-// Clears n floats (graph-capture safe, unlike a memset node).
+// Clears n floats (graph-capture safe, unlike a memset node): 16-byte
+// stores from the first 16-byte boundary, single floats before it and after
+// the last whole vector.
 __global__ void __launch_bounds__(kBlock) fill_zero(float* __restrict__ p, long long n,
                                                     int* __restrict__ status)
 {
     if (blockIdx.x == 0 && threadIdx.x == 0 && status) *status = 0;
-    const long long n4 = n / 4;
-    f4* p4 = reinterpret_cast<f4*>(p);
+    const long long gid = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
     const long long stride = static_cast<long long>(gridDim.x) * blockDim.x;
-    for (long long i = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x; i < n4;
-         i += stride)
-        p4[i] = f4(0.0f);
-    for (long long i = n4 * 4 + static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
-         i < n; i += stride)
-        p[i] = 0.0f;
+    const unsigned long long addr = reinterpret_cast<unsigned long long>(p);
+    long long head = (addr & 3ull) ? n : static_cast<long long>(((16ull - (addr & 15ull)) & 15ull) >> 2);
+    head = head < n ? head : n;
+    for (long long i = gid; i < head; i += stride) p[i] = 0.0f;
+    const long long n4 = (n - head) / 4;
+    f4* p4 = reinterpret_cast<f4*>(p + head);
+    for (long long i = gid; i < n4; i += stride) p4[i] = f4(0.0f);
+    for (long long i = head + n4 * 4 + gid; i < n; i += stride) p[i] = 0.0f;
 }
 
 __device__ __forceinline__ unsigned long long mix64(unsigned long long z)
@@ -816,11 +907,10 @@ void dispatch_main(hipStream_t st, const SpmmArgs& a, const Plan& p, int* status
 template <int VEC>
 void launch_zero(hipStream_t st, const SpmmArgs& a, const Plan& p, int* status)
 {
-    const long long blocks = (p.runs + kBlock - 1) / kBlock;
-    hipLaunchKernelGGL(zero_first_segments<VEC>, dim3(static_cast<unsigned>(blocks)),
-                       dim3(kBlock), 0, st, a.row_ptr, a.origin, a.n_rows,
-                       static_cast<long long>(a.nnz), a.tasks, static_cast<long long>(a.n_tasks),
-                       p.M, p.runs, a.K, a.C, status);
+    const long long blocks = (a.n_tasks + kBlock - 1) / kBlock;
+    hipLaunchKernelGGL(zero_split_rows<VEC>, dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0,
+                       st, a.row_ptr, a.origin, a.n_rows, static_cast<long long>(a.nnz), a.tasks,
+                       static_cast<long long>(a.n_tasks), p.M, a.K, a.C, status);
 }
 
 int pick_vec(const SpmmArgs& a)
@@ -904,6 +994,8 @@ cwlb_status launch_spmm_mean(cwlb_ctx* ctx, const SpmmArgs& a, bool zero_all, bo
     hipStream_t st = ctx->stream;
     (void)hipGetLastError();  // report only the launches below
     Plan p = make_plan(ctx, a, per_task);
+    if (a.n_tasks > kMaxGridBlocks * kBlock && a.K > 0)
+        return fail(CWLB_UNSUPPORTED, "spmm: more than 2^32 tasks");
     if (p.grid > kMaxGridBlocks && a.n_tasks > 0 && a.K > 0)
         return fail(CWLB_UNSUPPORTED,
                     "spmm: too many runs for one launch (more than 2^32 work-items); use more "

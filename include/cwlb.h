@@ -98,8 +98,8 @@ cwlb_status cwlb_ctx_create(int device, void* stream, cwlb_ctx** out);
 cwlb_status cwlb_ctx_destroy(cwlb_ctx* ctx);
 cwlb_status cwlb_ctx_set_stream(cwlb_ctx* ctx, void* stream);
 /* Waits for the context's stream; then reports, as CWLB_INVALID_ARG, a bad
- * column index or origin entry that the last aggregation met (asynchronous
- * calls cannot report it themselves). */
+ * column index, origin entry or row offset that the last aggregation met
+ * (asynchronous calls cannot report it themselves). */
 cwlb_status cwlb_ctx_synchronize(cwlb_ctx* ctx);
 cwlb_status cwlb_ctx_device_info(cwlb_ctx* ctx, cwlb_device_info* out);
 /* Schedule of later SpMM calls on this context: tasks executed per wave
@@ -183,25 +183,34 @@ cwlb_status cwlb_ctx_last_launch(cwlb_ctx* ctx, cwlb_launch_info* out);
  * C[n_rows*K].
  *
  * Preconditions checked on the host: n_rows >= 0, nnz >= 0, K >= 0,
- * n_tasks >= 0, non-null pointers for non-empty arrays.  Task entries are
- * validated on the device-side for bounds (row ranges clamped as in the
- * reference, parallelMatrix.cpp:169-176); column indices must be < h_rows.
+ * n_tasks >= 0, non-null pointers for non-empty arrays.  On the device:
+ * task row ranges are clamped as in the reference (parallelMatrix.cpp:
+ * 169-176); a column index outside [0, h_rows), an origin entry outside
+ * [0, n_rows) or a row whose offsets leave [0, nnz] or decrease is skipped
+ * and reported as CWLB_INVALID_ARG (by this call when it synchronises, else
+ * by cwlb_ctx_synchronize).
  * With the flag CWLB_SPMM_ZERO_OUTPUT the whole of C is cleared first (the
- * reference's host-side Zero(), parallelMatrix.cpp:112), which makes any
- * task list behave as in the reference; without it, rows that no task
- * touches keep their previous contents (a partition from
- * cwlb_partition touches every row).
+ * reference's host-side Zero(), parallelMatrix.cpp:112).  Then every task
+ * list in which no two tasks share a nonzero -- in any order, with gaps --
+ * gives the reference's result; lists whose tasks overlap need
+ * CWLB_SPMM_PER_TASK as well.  Without the flag, rows whose first nonzero
+ * no task covers keep their previous contents (a partition from
+ * cwlb_partition covers every row).
  * K == 0 or n_tasks == 0: C is cleared (when CWLB_SPMM_ZERO_OUTPUT is set)
  * and timings are 0, as the reference returns a zero matrix with time 0
  * (parallelMatrix.cpp:80-83, 101-104).
- * timing may be NULL (asynchronous: bad column indices or origin entries
- * are then reported by the next cwlb_ctx_synchronize); otherwise the call
+ * timing may be NULL (asynchronous: the bad entries above are then
+ * reported by the next cwlb_ctx_synchronize); otherwise the call
  * synchronises.  The default and CWLB_SPMM_ZERO_OUTPUT paths launch kernels
  * only (no memset nodes, no allocation), so an asynchronous call can be
  * captured into a HIP graph.  Under capture the run order (run_order = 2)
  * and the cache hints are reused when an earlier call built them for the
  * same arrays, and otherwise left out (task order, normal cache policy);
- * the results are the same either way.
+ * the results are the same either way.  A captured graph stays valid until
+ * cwlb_ctx_destroy: a run order or hint array that a capture used is never
+ * rewritten or freed by later calls on the context (a rebuild goes into a
+ * new buffer), so replays may be interleaved with eager calls on other
+ * task or column arrays.
  *
  * cwlb_spmm_mean_f32 mirrors spmmKernel: K > max work-group size (1024)
  * returns CWLB_INVALID_ARG (parallelMatrix.cpp:84-88).
@@ -210,11 +219,14 @@ cwlb_status cwlb_ctx_last_launch(cwlb_ctx* ctx, cwlb_launch_info* out);
 #define CWLB_SPMM_ZERO_OUTPUT 0x1u
 /* Execute exactly one task per wave, each partial chunk added atomically
  * (the reference's structure).  Without this flag a wave executes a run of
- * consecutive tasks, chosen from the task count and the CU count; a run is
- * itself a task (the union of consecutive tasks is contiguous), so rows
- * split only inside a run are reduced in registers and stored, and the
- * feature columns may be split across the XCDs.  Both modes give the same
- * result up to float rounding. */
+ * consecutive tasks (run length chosen from the task count and the CU
+ * count), and the feature columns may be split across the XCDs.  Inside a
+ * run, each stretch of tasks in which every task starts where the previous
+ * one ended (the partition's lists consist of such stretches) is executed
+ * as one task: rows split only inside it are reduced in registers and
+ * stored.  A task that does not continue its predecessor, or a malformed
+ * one, starts a new stretch.  For task lists without overlapping tasks both
+ * modes give the same result up to float rounding. */
 #define CWLB_SPMM_PER_TASK 0x2u
 
 cwlb_status cwlb_spmm_mean_f32(cwlb_ctx* ctx, const int32_t* row_ptr, const int32_t* col_idx,
@@ -261,7 +273,9 @@ cwlb_status cwlb_ctx_tune_schedule(cwlb_ctx* ctx, const int32_t* row_ptr, const 
 /* Host-pointer form: copies the inputs to the device, runs the call, copies
  * C back (the reference's per-call sycl::buffer behaviour,
  * parallelMatrix.cpp:115-121).  C is always cleared first.  Dispatches on K
- * like run_single_s (main.cpp:359-365).  Timing covers the kernels only.
+ * like run_single_s (main.cpp:359-365).  A task list that does not tile the
+ * nonzeros in order runs one task per wave, so every list, overlapping ones
+ * included, gives the reference's result.  Timing covers the kernels only.
  * The host arrays may be pageable: transfers go through two 64 MiB pinned
  * staging buffers that the context allocates at its first host-pointer call
  * and keeps until cwlb_ctx_destroy, filled and drained by up to 8 host

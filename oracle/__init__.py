@@ -63,8 +63,15 @@ def lib():
     return _LIB
 
 
+def ref_built() -> bool:
+    """Whether oracle/_ref/libcwlb_ref.so exists (checked without loading it)."""
+    return os.path.exists(os.path.join(HERE, "_ref", "libcwlb_ref.so"))
+
+
 def ref():
-    """The reference's own partition / S-selection / cost-file functions, or None."""
+    """The reference's own partition / S-selection / cost-file functions, or
+    None.  Loaded on first use, so that merely collecting tests does not map
+    the library."""
     global _REF
     if _REF is None:
         path = os.path.join(HERE, "_ref", "libcwlb_ref.so")

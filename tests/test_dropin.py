@@ -18,7 +18,6 @@ from cwlb_amd import workloads
 from dropin_util import (BIN, ProbeError, probe, read_csr, read_order, write_csr, write_f32,
                          write_order)
 
-REF = oracle.ref()
 
 
 # ------------------------------------------------------------------ reorder
@@ -89,7 +88,7 @@ def test_partition_matches_oracle_and_reference(tmp_path, cfg):
             cap, tasks = run_partition(tmp_path, order, costs, S)
             assert cap == oracle.capacity_from_s(S, costs)
             assert np.array_equal(tasks, oracle.partition(order[1], costs, cap))
-            if REF is not None:
+            if oracle.ref() is not None:
                 assert np.array_equal(tasks, oracle.ref_partition(order[1], costs, cap))
 
 
@@ -291,7 +290,7 @@ def test_cost_file_roundtrip(tmp_path):
     c4 = (0.004519, 0.015617, 0.010667, 0.540499)
     assert probe("costs-save", p, 0, 6, *c4).split()[1] == "1"
     assert p.read_text() == oracle.format_costs(c4, 6)
-    if REF is not None:
+    if oracle.ref() is not None:
         assert p.read_text() == oracle.ref_format_costs(c4, 6)
     out = probe("costs-read", p).split()
     assert out[1] == "1" and [float(x) for x in out[2:6]] == list(c4) and out[7] == "7"
@@ -419,5 +418,5 @@ def test_partition_decomposition_workloads(tmp_path, cfg):
         got = run_partition_emul(tmp_path, order, SKEWED_COSTS, S)
         cap = oracle.capacity_from_s(S, SKEWED_COSTS)
         assert np.array_equal(got, oracle.partition(order[1], SKEWED_COSTS, cap))
-        if REF is not None:
+        if oracle.ref() is not None:
             assert np.array_equal(got, oracle.ref_partition(order[1], SKEWED_COSTS, cap))

@@ -440,6 +440,105 @@ def test_unsorted_graph_custom_tasks(gpu_ctx, rng):
         check(got, ref32)
 
 
+def big_random_graph(n, max_deg, seed):
+    rng = np.random.default_rng(seed)
+    deg = rng.integers(0, max_deg + 1, n)
+    rp = np.concatenate([[0], np.cumsum(deg)]).astype(np.int32)
+    ci = rng.integers(0, n, rp[-1]).astype(np.int32)
+    val = rng.uniform(-1, 1, rp[-1]).astype(np.float32)
+    return custom_graph(rp, ci, val)
+
+
+@pytest.mark.parametrize("order", ["shuffled", "reversed", "in_order"])
+def test_many_per_row_tasks_in_any_order(gpu_ctx, order):
+    """200,000 one-row tasks, in task order, reversed and shuffled: enough
+    tasks that the automatic schedule runs several tasks per wave.  Runs of
+    tasks that do not continue one another execute task by task, so every
+    order gives the reference's result (the rows no longer neighbour each
+    other, and a run taken as one range would compute other rows)."""
+    g = big_random_graph(200_000, 12, 21)
+    H = synth.features(g.n, 32, 3)
+    origin, rp, ci, val = capi.reorder_by_degree(g.row_ptr, g.col_idx, g.val)
+    base = workloads.Prepared(g.n, g.nnz, origin, rp, ci, val, None, 0, 0.0)
+    per_row = np.stack([np.arange(g.n), np.arange(1, g.n + 1), np.zeros(g.n), np.zeros(g.n)],
+                       1).astype(np.int32)
+    if order == "shuffled":
+        per_row = per_row[np.random.default_rng(5).permutation(g.n)]
+    elif order == "reversed":
+        per_row = per_row[::-1].copy()
+    base.tasks = per_row
+    got, _ = run_gpu(gpu_ctx, base, H)
+    assert gpu_ctx.last_launch()["tasks_per_wave"] > 1
+    check(got, oracle.spmm_mean_f32(rp, ci, val, origin, H, per_row))
+    check(got, oracle.spmm_mean_f64(g.row_ptr, g.col_idx, g.val, H))
+
+
+@pytest.mark.parametrize("how", ["shuffled", "swapped_pairs", "gaps"])
+@pytest.mark.parametrize("m", [0, 64, 5])
+def test_partition_list_out_of_order(gpu_ctx, how, m):
+    """The partition's task list (split rows included) shuffled, with pairs
+    of neighbours swapped, or with a fifth of the tasks dropped, at the
+    automatic run length and at 64 and 5 tasks per wave: with the full clear
+    of CWLB_SPMM_ZERO_OUTPUT the result is the reference's for that list."""
+    rng = np.random.default_rng(len(how) + m)
+    g = workloads.small(4, seed=23)
+    H = synth.features(g.n, 64, 8)
+    p = problem(g, SKEWED_COSTS, 3)
+    t = p.tasks.copy()
+    if how == "shuffled":
+        t = t[rng.permutation(len(t))]
+    elif how == "swapped_pairs":
+        idx = np.arange(len(t))
+        sw = rng.choice(len(t) // 2, len(t) // 8, replace=False) * 2
+        idx[sw], idx[sw + 1] = sw + 1, sw
+        t = t[idx]
+    else:
+        t = t[rng.random(len(t)) > 0.2]
+    p.tasks = np.ascontiguousarray(t)
+    gpu_ctx.set_schedule(m, 0)
+    try:
+        got, _ = run_gpu(gpu_ctx, p, H, flags=capi.ZERO_OUTPUT)
+    finally:
+        gpu_ctx.set_schedule(0, 0)
+    check(got, oracle.spmm_mean_f32(p.row_ptr, p.col_idx, p.val, p.origin, H, p.tasks))
+    if how != "gaps":
+        # Every row's first nonzero is in the list: without the full clear
+        # the clearing pass alone defines every row (C starts as NaN).
+        gpu_ctx.set_schedule(m, 0)
+        try:
+            got, _ = run_gpu(gpu_ctx, p, H)
+        finally:
+            gpu_ctx.set_schedule(0, 0)
+        check(got, oracle.spmm_mean_f32(p.row_ptr, p.col_idx, p.val, p.origin, H, p.tasks))
+
+
+@pytest.mark.parametrize("bad", ["decreasing", "beyond_nnz", "negative"])
+def test_malformed_row_offsets_are_reported(gpu_ctx, bad):
+    """Row offsets that decrease, pass nnz or are negative are met on the
+    device without any access outside the arrays and reported as
+    CWLB_INVALID_ARG; a good call afterwards clears the report."""
+    g = workloads.small(1, seed=2)
+    H = synth.features(g.n, 32, 3)
+    p = problem(g, UNIT_COSTS, 6)
+    rp = p.row_ptr.copy()
+    r = len(rp) // 2
+    if bad == "decreasing":
+        rp[r] = rp[r + 1] + 3
+    elif bad == "beyond_nnz":
+        rp[-1] = p.nnz + 100
+    else:
+        rp[r] = -5
+    good = p.row_ptr
+    p.row_ptr = rp
+    with pytest.raises(capi.CwlbError) as e:
+        run_gpu(gpu_ctx, p, H)
+    assert e.value.status == capi.INVALID_ARG
+    assert b"row_ptr" in capi.lib().cwlb_last_error()
+    p.row_ptr = good
+    got, _ = run_gpu(gpu_ctx, p, H)
+    check(got, oracle.spmm_mean_f32(p.row_ptr, p.col_idx, p.val, p.origin, H, p.tasks))
+
+
 def test_zero_output_flag_with_partial_cover(gpu_ctx):
     """ZERO_OUTPUT reproduces the reference's zeroed C for rows no task touches."""
     g = workloads.small(1, seed=2)
@@ -523,6 +622,21 @@ def test_host_pointer_entry(gpu_ctx):
     assert t.main_us > 0
 
 
+def test_host_pointer_entry_overlapping_and_shuffled_tasks(gpu_ctx):
+    """The host-pointer entry (the drop-in spmmKernel) takes any task list:
+    the partition twice over (every nonzero covered twice: whole rows are
+    stored twice, split rows receive both sets of partial sums) and the
+    partition shuffled both give the reference's task-at-a-time result."""
+    g = workloads.small(4, seed=8)
+    H = synth.features(g.n, 64, 3)
+    p = problem(g, SKEWED_COSTS, 5)
+    rng = np.random.default_rng(2)
+    for tasks in (np.concatenate([p.tasks, p.tasks]), p.tasks[rng.permutation(len(p.tasks))]):
+        tasks = np.ascontiguousarray(tasks)
+        got, _ = gpu_ctx.spmm_host(p.row_ptr, p.col_idx, p.val, p.origin, H, tasks)
+        check(got, oracle.spmm_mean_f32(p.row_ptr, p.col_idx, p.val, p.origin, H, tasks))
+
+
 def test_host_pointer_entry_multi_chunk(gpu_ctx):
     """Inputs and output larger than one 64 MiB staging buffer (H and C of
     about 160 MB each: several chunks through both buffers), then a small
@@ -546,7 +660,9 @@ def test_host_pointer_entry_multi_chunk(gpu_ctx):
 def test_misaligned_feature_and_output_pointers(gpu_ctx, K, h_off, c_off):
     """H and C handed over as views that start 4 or 8 bytes past a 16-byte
     boundary: the kernel falls back to 8- or 4-byte lanes and still matches
-    the oracle; the floats around the output view are left untouched."""
+    the oracle, also with the full clear of CWLB_SPMM_ZERO_OUTPUT (single
+    floats up to the first 16-byte boundary); the floats around the output
+    view are left untouched."""
     torch = torch_mod()
     g = workloads.small(4, seed=21)
     H = synth.features(g.n, K, 4)
@@ -558,13 +674,16 @@ def test_misaligned_feature_and_output_pointers(gpu_ctx, K, h_off, c_off):
     d_H = h_buf[h_off:h_off + g.n * K].view(g.n, K)
     c_buf = torch.full((g.n * K + 8,), -5.0, dtype=torch.float32, device="cuda")
     d_C = c_buf[c_off:c_off + g.n * K].view(g.n, K)
-    gpu_ctx.spmm(d_rp, d_ci, d_v, d_o, g.n, g.nnz, d_H, g.n, K, d_t, len(p.tasks), d_C)
     ref32, ref64 = oracle_pair(p, g, H)
-    got = d_C.cpu().numpy()
-    check(got, ref32)
-    check(got, ref64)
-    rest = torch.cat([c_buf[:c_off], c_buf[c_off + g.n * K:]]).cpu().numpy()
-    assert np.all(rest == -5.0)
+    for flags in (0, capi.ZERO_OUTPUT):
+        c_buf.fill_(-5.0)
+        gpu_ctx.spmm(d_rp, d_ci, d_v, d_o, g.n, g.nnz, d_H, g.n, K, d_t, len(p.tasks), d_C,
+                     flags=flags)
+        got = d_C.cpu().numpy()
+        check(got, ref32)
+        check(got, ref64)
+        rest = torch.cat([c_buf[:c_off], c_buf[c_off + g.n * K:]]).cpu().numpy()
+        assert np.all(rest == -5.0)
 
 
 @pytest.mark.parametrize("K", [32, 128])
@@ -946,6 +1065,69 @@ def _capture_and_replay(gpu_ctx, torch, g, K, p, d, H, C, flags, eager_cfg, capt
         _ = (H * 2.0).sum().item()  # eager work between replays
     ref32 = oracle.spmm_mean_f32(p.row_ptr, p.col_idx, p.val, p.origin, H.cpu().numpy(), p.tasks)
     np.testing.assert_allclose(C.cpu().numpy(), ref32, rtol=RTOL, atol=ATOL)
+
+
+def test_graph_replay_after_rebuild_on_other_arrays(gpu_ctx):
+    """A graph captured with a run order and cache hints built by an eager
+    call keeps working after eager calls on the same context rebuild both
+    for another problem (fewer runs, another column array): the rebuild
+    goes into new buffers, and every replay still gives the first problem's
+    result, interleaved with the second problem's eager calls."""
+    torch = torch_mod()
+    K = 64
+    g1 = workloads.small(4, seed=21)
+    p1 = problem(g1, SKEWED_COSTS, 9)
+    g2 = workloads.small(4, seed=22)
+    p2 = problem(g2, SKEWED_COSTS, 40)
+    d1 = [dev(x) for x in (p1.row_ptr, p1.col_idx, p1.val, p1.origin)]
+    d1.append(dev(np.ascontiguousarray(p1.tasks, np.int32).reshape(-1)))
+    d2 = [dev(x) for x in (p2.row_ptr, p2.col_idx, p2.val, p2.origin)]
+    d2.append(dev(np.ascontiguousarray(p2.tasks, np.int32).reshape(-1)))
+    H1, H2 = synth.features(g1.n, K, 4), synth.features(g2.n, K, 5)
+    dH1, dH2 = dev(H1), dev(H2)
+    C1 = torch.zeros((g1.n, K), dtype=torch.float32, device="cuda")
+    C2 = torch.zeros((g2.n, K), dtype=torch.float32, device="cuda")
+    ref1 = oracle.spmm_mean_f32(p1.row_ptr, p1.col_idx, p1.val, p1.origin, H1, p1.tasks)
+    ref2 = oracle.spmm_mean_f32(p2.row_ptr, p2.col_idx, p2.val, p2.origin, H2, p2.tasks)
+
+    def call(d, g, p, dH, C, **kw):
+        gpu_ctx.spmm(d[0], d[1], d[2], d[3], g.n, g.nnz, dH, g.n, K, d[4], len(p.tasks), C,
+                     **kw)
+
+    gpu_ctx.set_schedule(4, 0)
+    gpu_ctx.set_locality(2, 0)
+    gpu_ctx.set_cache_hints(HOT64)
+    try:
+        call(d1, g1, p1, dH1, C1)  # builds the run order and the hints for problem 1
+        info = gpu_ctx.last_launch()
+        assert (info["run_order"], info["cache_hints"]) == (2, 1), info
+        graph = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            gpu_ctx.set_stream(side.cuda_stream)
+            with torch.cuda.graph(graph, stream=side):
+                call(d1, g1, p1, dH1, C1, timed=False)
+        gpu_ctx.set_stream(torch.cuda.current_stream().cuda_stream)
+        info = gpu_ctx.last_launch()
+        assert (info["run_order"], info["cache_hints"]) == (2, 1), info
+        torch.cuda.synchronize()
+        for i in range(3):
+            C2.fill_(float("nan"))
+            call(d2, g2, p2, dH2, C2)  # rebuilds order and hints for problem 2
+            info = gpu_ctx.last_launch()
+            assert (info["run_order"], info["cache_hints"]) == (2, 1), info
+            check(C2.cpu().numpy(), ref2)
+            C1.fill_(float("nan"))
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            check(C1.cpu().numpy(), ref1)
+            gpu_ctx.set_locality(2, 0)  # forget the order: the next call sorts again
+    finally:
+        gpu_ctx.set_schedule(0, 0)
+        gpu_ctx.set_locality(0, 0)
+        gpu_ctx.set_cache_hints(0)
 
 
 def test_tune_schedule(gpu_ctx):

@@ -19,8 +19,7 @@ import oracle
 from conftest import SKEWED_COSTS, UNIT_COSTS
 from cwlb_amd import synth, workloads
 
-REF = oracle.ref()
-need_ref = pytest.mark.skipif(REF is None, reason="oracle/_ref not built (no /root/reference)")
+need_ref = pytest.mark.skipif(not oracle.ref_built(), reason="oracle/_ref not built (no /root/reference)")
 
 
 def rp_of(degs):
@@ -50,7 +49,7 @@ def test_partition_known_answers(degs, expected):
     cap = oracle.capacity_from_s(4, UNIT_COSTS)
     assert cap == 4.5
     assert tasks_list(oracle.partition(rp_of(degs), UNIT_COSTS, cap)) == expected
-    if REF is not None:
+    if oracle.ref() is not None:
         assert tasks_list(oracle.ref_partition(rp_of(degs), UNIT_COSTS, cap)) == expected
 
 
@@ -292,7 +291,7 @@ def test_s_selection_readme_examples():
 @need_ref
 def test_s_selection_matches_reference(rng):
     import ctypes as C
-    R = REF
+    R = oracle.ref()
     for _ in range(3000):
         nnz = int(rng.integers(0, 2**40))
         out_a, out_b = np.zeros(3, np.int32), np.zeros(3, np.int32)
@@ -352,7 +351,7 @@ def test_planted_partition_mistakes_are_caught(m):
         for degs, expected in KATS:
             if tasks_list(oracle.partition(rp_of(degs), UNIT_COSTS, cap)) != expected:
                 caught = True
-        if REF is not None and not caught:
+        if oracle.ref() is not None and not caught:
             rng = np.random.default_rng(0)
             for _ in range(500):
                 rp = rp_of(random_degrees(rng))

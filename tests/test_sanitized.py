@@ -20,7 +20,6 @@ from dropin_util import ProbeError, write_csr, write_order
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 SAN = os.path.join(HERE, "cxx", "bin", "dropin_probe_san")
-REF = oracle.ref()
 ENV = dict(os.environ, ASAN_OPTIONS="detect_leaks=0:abort_on_error=0:exitcode=86",
            UBSAN_OPTIONS="print_stacktrace=1:halt_on_error=1:exitcode=87")
 SETTINGS = settings(max_examples=60, deadline=None,
@@ -60,7 +59,7 @@ def test_partition_fuzz(tmp_path, degs, costs, S):
     got = np.frombuffer(raw[8:], np.int32).reshape(-1, 4)
     assert cap == oracle.capacity_from_s(S, costs)
     assert np.array_equal(got, oracle.partition(rp, costs, cap))
-    if REF is not None:
+    if oracle.ref() is not None:
         assert np.array_equal(got, oracle.ref_partition(rp, costs, cap))
     # the GPU partition's decomposition, for the costs it takes
     try:
