@@ -27,6 +27,7 @@ EXPORTS = [
     "cwlb_ctx_last_launch", "cwlb_ctx_set_occupancy", "cwlb_ctx_get_occupancy",
     "cwlb_ctx_tune_schedule",
     "cwlb_spmm_mean_f32", "cwlb_spmm_mean_f32_large_k", "cwlb_spmm_mean_f32_host",
+    "cwlb_spmm_mean_f32_noalloc",
     "cwlb_reorder_by_degree", "cwlb_reorder_by_degree_device", "cwlb_partition",
     "cwlb_partition_device",
     "cwlb_capacity_from_s", "cwlb_wave_based_s", "cwlb_recommended_candidate_w",
@@ -121,6 +122,8 @@ def lib():
         L.cwlb_spmm_mean_f32_large_k.argtypes = spmm
         L.cwlb_spmm_mean_f32_host.argtypes = [vp, vp, vp, vp, vp, i32, i64, vp, i64, i32, vp, i64,
                                               vp, C.POINTER(Timing)]
+        L.cwlb_spmm_mean_f32_noalloc.argtypes = [vp, vp, vp, vp, vp, i32, i64, vp, i64, i32, vp,
+                                                 i64, vp, u32, i32, i32, i32]
         L.cwlb_reorder_by_degree.argtypes = [i32, i64, vp, vp, vp, vp, vp, vp, vp]
         L.cwlb_reorder_by_degree_device.argtypes = [vp, i32, i64, vp, vp, vp, vp, vp, vp, vp]
         L.cwlb_partition.argtypes = [vp, i32, C.POINTER(CostParams), C.c_double, vp, i64,
@@ -254,6 +257,16 @@ def read_costs(path):
 
 
 # ---------------------------------------------------------------- device-side
+def spmm_noalloc(stream, row_ptr, col_idx, val, origin, n_rows, nnz, H, h_rows, K, tasks,
+                 n_tasks, C_out, flags=0, tasks_per_wave=0, feature_slices=0, synchronize=True):
+    """cwlb_spmm_mean_f32_noalloc on device arrays (no context, nothing
+    allocated); stream is a hipStream_t handle (0 = the null stream)."""
+    check(lib().cwlb_spmm_mean_f32_noalloc(
+        C.c_void_p(stream or None), _ptr(row_ptr), _ptr(col_idx), _ptr(val), _ptr(origin),
+        int(n_rows), int(nnz), _ptr(H), int(h_rows), int(K), _ptr(tasks), int(n_tasks),
+        _ptr(C_out), int(flags), int(tasks_per_wave), int(feature_slices), int(bool(synchronize))))
+
+
 class Context:
     """A libcwlb context on one device, launching on `stream` (hipStream_t handle)."""
 

@@ -288,6 +288,32 @@ cwlb_status cwlb_spmm_mean_f32_host(cwlb_ctx* ctx, const int32_t* row_ptr,
                                     const cwlb_task* tasks, int64_t n_tasks, float* C,
                                     cwlb_timing* timing);
 
+/* Allocation-free form of cwlb_spmm_mean_f32, with no counterpart in the
+ * reference: for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).  It
+ * needs no context: it runs on the current HIP device and the given stream
+ * (NULL = the null stream), with the automatic schedule or the given tasks
+ * per wave and feature slices (as cwlb_ctx_set_schedule; 0 = automatic), in
+ * task order and without cache hints.  Any K is accepted (both
+ * cwlb_spmm_mean_f32's range and the large-K entry's); flags and results
+ * are those of cwlb_spmm_mean_f32.  It calls no hipMalloc, hipFree or other
+ * allocating routine: the kernels' status word lives in a 256-byte device
+ * array of the library (one per GPU, kept until the process ends, located
+ * on a device's first call); its size does not depend on the inputs, so no
+ * input is too large for it.  synchronize != 0: the call waits for the
+ * stream and reports a bad column index, origin entry or row offset as
+ * CWLB_INVALID_ARG; 0: asynchronous, such entries are skipped unreported.
+ * All calls on one GPU share that status word, which each call resets:
+ * calls that overlap on one GPU (different streams) may report each
+ * other's errors. */
+cwlb_status cwlb_spmm_mean_f32_noalloc(void* stream, const int32_t* row_ptr,
+                                       const int32_t* col_idx, const float* val,
+                                       const int32_t* origin, int32_t n_rows, int64_t nnz,
+                                       const float* H, int64_t h_rows, int32_t K,
+                                       const cwlb_task* tasks, int64_t n_tasks, float* C,
+                                       uint32_t flags, int32_t tasks_per_wave,
+                                       int32_t feature_slices, int32_t synchronize);
+
 /* ----------------------------------------------------------- preprocessing
  * Degree reordering, sortCSRByDegreeDPLCPU (reference main.cpp:197-278):
  * rows ordered by (degree, original id) ascending; origin[new] = old;

@@ -1,0 +1,96 @@
+"""cwlb_spmm_mean_f32_noalloc against cwlb_spmm_mean_f32.
+
+The allocation-free entry point (no context, status word in the library's
+own device array) must give the context entry point's result on the same
+inputs, to the parity tolerance, call after call: two calls in a row, the
+second on a smaller problem, then error reporting and the schedule
+arguments.  Everything goes through the C ABI.
+"""
+import numpy as np
+import pytest
+
+import oracle
+from conftest import SKEWED_COSTS, UNIT_COSTS
+from cwlb_amd import capi, synth, workloads
+
+pytestmark = pytest.mark.gpu
+
+RTOL, ATOL = 1e-5, 1e-6
+
+
+def _dev(torch, a):
+    a = np.ascontiguousarray(a)
+    if a.size == 0:
+        a = np.zeros(1, a.dtype)
+    return torch.from_numpy(a).cuda()
+
+
+def _inputs(torch, cfg, seed, K, S, costs):
+    g = workloads.small(cfg, seed=seed)
+    p = workloads.prepare(g, costs, S)
+    H = synth.features(g.n, K, seed)
+    d = [_dev(torch, x) for x in (p.row_ptr, p.col_idx, p.val, p.origin)]
+    d_t = _dev(torch, np.ascontiguousarray(p.tasks, np.int32).reshape(-1))
+    return g, p, H, d, _dev(torch, H), d_t
+
+
+def _both(gpu_ctx, torch, g, p, d, d_H, d_t, K, flags=0, m=0, sl=0):
+    """(no-alloc result, context result) of one problem."""
+    stream = torch.cuda.current_stream().cuda_stream
+    C_na = torch.full((g.n, K), float("nan"), dtype=torch.float32, device="cuda")
+    capi.spmm_noalloc(stream, d[0], d[1], d[2], d[3], g.n, g.nnz, d_H, g.n, K, d_t,
+                      len(p.tasks), C_na, flags=flags, tasks_per_wave=m, feature_slices=sl)
+    C_ctx = torch.full((g.n, K), float("nan"), dtype=torch.float32, device="cuda")
+    gpu_ctx.set_schedule(m, sl)
+    try:
+        gpu_ctx.spmm(d[0], d[1], d[2], d[3], g.n, g.nnz, d_H, g.n, K, d_t, len(p.tasks), C_ctx,
+                     flags=flags, large_k=K > 1024)
+    finally:
+        gpu_ctx.set_schedule(0, 0)
+    return C_na.cpu().numpy(), C_ctx.cpu().numpy()
+
+
+def test_noalloc_matches_context_entry_twice(gpu_ctx):
+    """A larger problem, then a smaller one, on the same device array."""
+    import torch
+    for cfg, seed, K, S in ((4, 31, 128, 9), (1, 5, 32, 6)):
+        g, p, H, d, d_H, d_t = _inputs(torch, cfg, seed, K, S, SKEWED_COSTS)
+        got, want = _both(gpu_ctx, torch, g, p, d, d_H, d_t, K)
+        np.testing.assert_allclose(got, want, rtol=RTOL, atol=ATOL)
+        ref = oracle.spmm_mean_f32(p.row_ptr, p.col_idx, p.val, p.origin, H, p.tasks)
+        np.testing.assert_allclose(got, ref, rtol=RTOL, atol=ATOL)
+
+
+@pytest.mark.parametrize("flags,m,sl", [(0, 8, 2), (capi.ZERO_OUTPUT, 0, 0),
+                                        (capi.PER_TASK, 0, 0), (0, 64, 4)])
+def test_noalloc_flags_and_schedule(gpu_ctx, flags, m, sl):
+    import torch
+    g, p, H, d, d_H, d_t = _inputs(torch, 4, 12, 64, 5, UNIT_COSTS)
+    got, want = _both(gpu_ctx, torch, g, p, d, d_H, d_t, 64, flags=flags, m=m, sl=sl)
+    np.testing.assert_allclose(got, want, rtol=RTOL, atol=ATOL)
+
+
+def test_noalloc_large_k_and_errors(gpu_ctx):
+    """K above the work-group limit, a bad column index reported (and
+    cleared by the next good call), and argument errors."""
+    import torch
+    g, p, H, d, d_H, d_t = _inputs(torch, 1, 9, 1100, 5, UNIT_COSTS)
+    got, want = _both(gpu_ctx, torch, g, p, d, d_H, d_t, 1100)
+    np.testing.assert_allclose(got, want, rtol=RTOL, atol=ATOL)
+    stream = torch.cuda.current_stream().cuda_stream
+    C = torch.zeros((g.n, 1100), dtype=torch.float32, device="cuda")
+    ci = p.col_idx.copy()
+    ci[len(ci) // 2] = g.n + 3
+    bad = _dev(torch, ci)
+    with pytest.raises(capi.CwlbError) as e:
+        capi.spmm_noalloc(stream, d[0], bad, d[2], d[3], g.n, g.nnz, d_H, g.n, 1100, d_t,
+                          len(p.tasks), C)
+    assert e.value.status == capi.INVALID_ARG
+    capi.spmm_noalloc(stream, d[0], d[1], d[2], d[3], g.n, g.nnz, d_H, g.n, 1100, d_t,
+                      len(p.tasks), C)
+    np.testing.assert_allclose(C.cpu().numpy(), want, rtol=RTOL, atol=ATOL)
+    for kw in ({"tasks_per_wave": -1}, {"feature_slices": 3}):
+        with pytest.raises(capi.CwlbError) as e:
+            capi.spmm_noalloc(stream, d[0], d[1], d[2], d[3], g.n, g.nnz, d_H, g.n, 1100, d_t,
+                              len(p.tasks), C, **kw)
+        assert e.value.status == capi.INVALID_ARG
