@@ -128,9 +128,11 @@ struct Buf {
 }  // namespace
 
 cwlb_status run_calibration(cwlb_ctx* ctx, int32_t K, int32_t repeat, int32_t WI, int32_t load_MB,
-                            int32_t atomic_writers, cwlb_cost_params* out)
+                            int32_t atomic_writers, cwlb_cost_params* out,
+                            cwlb_calibration_report* report)
 {
     hipStream_t st = ctx->stream;
+    cwlb_calibration_report rep{};
     *out = cwlb_cost_params{};
     out->K = K;
     out->WI = WI;
@@ -149,6 +151,8 @@ cwlb_status run_calibration(cwlb_ctx* ctx, int32_t K, int32_t repeat, int32_t WI
             nothing, &ms);
         if (s != CWLB_OK) return s;
         out->C_compute_ns = (ms * 1e6) / static_cast<double>(WI) / static_cast<double>(K) * 10;
+        rep.compute_ms = ms;
+        rep.compute_ops = static_cast<int64_t>(WI) * K;
     }
     {  // load
         const size_t total_floats = static_cast<size_t>(load_MB) * 1024ull * 1024ull / sizeof(float);
@@ -180,6 +184,9 @@ cwlb_status run_calibration(cwlb_ctx* ctx, int32_t K, int32_t repeat, int32_t WI
             nothing, &ms);
         if (s != CWLB_OK) return s;
         out->C_load_ns = (ms * 1e6) / static_cast<double>(WI) / static_cast<double>(K) * 10;
+        rep.load_ms = ms;
+        rep.load_ops = static_cast<int64_t>(WI) * K;
+        rep.load_bytes = static_cast<int64_t>(WI) * K * 4;
     }
     {  // store
         Buf<float> obuf;
@@ -192,6 +199,9 @@ cwlb_status run_calibration(cwlb_ctx* ctx, int32_t K, int32_t repeat, int32_t WI
             nothing, &ms);
         if (s != CWLB_OK) return s;
         out->C_store_ns = (ms * 1e6) / static_cast<double>(WI) / static_cast<double>(K) * 10;
+        rep.store_ms = ms;
+        rep.store_ops = static_cast<int64_t>(WI) * K;
+        rep.store_bytes = static_cast<int64_t>(WI) * K * 4;
     }
     {  // atomic
         const int gpr = std::max(1, atomic_writers);
@@ -227,8 +237,11 @@ cwlb_status run_calibration(cwlb_ctx* ctx, int32_t K, int32_t repeat, int32_t WI
         const double ops = static_cast<double>(total_groups) * static_cast<double>(K_block);
         out->C_atomic_ns = (ms * 1e6) / ops * 10.0;
         out->atomic_writers_per_addr = gpr;
+        rep.atomic_ms = ms;
+        rep.atomic_ops = total_groups * K_block;
     }
     CWLB_HIP_TRY(hipStreamSynchronize(st));
+    if (report) *report = rep;
     return CWLB_OK;
 }
 

@@ -734,14 +734,21 @@ cwlb_status cwlb_partition_device(cwlb_ctx* ctx, const int32_t* row_ptr, int32_t
                             n_tasks);
 }
 
-cwlb_status cwlb_calibrate(cwlb_ctx* ctx, int32_t K, int32_t repeat, int32_t WI, int32_t load_MB,
-                           int32_t atomic_writers, cwlb_cost_params* out)
+cwlb_status cwlb_calibrate_report(cwlb_ctx* ctx, int32_t K, int32_t repeat, int32_t WI,
+                                  int32_t load_MB, int32_t atomic_writers, cwlb_cost_params* out,
+                                  cwlb_calibration_report* report)
 {
     if (!ctx || !out) return fail(CWLB_INVALID_ARG, "null argument");
     if (K <= 0 || repeat <= 0 || WI <= 0 || load_MB <= 0 || atomic_writers <= 0)
         return fail(CWLB_INVALID_ARG, "All microbenchmark parameters must be positive.");
     DeviceGuard g(ctx->device);
-    return run_calibration(ctx, K, repeat, WI, load_MB, atomic_writers, out);
+    return run_calibration(ctx, K, repeat, WI, load_MB, atomic_writers, out, report);
+}
+
+cwlb_status cwlb_calibrate(cwlb_ctx* ctx, int32_t K, int32_t repeat, int32_t WI, int32_t load_MB,
+                           int32_t atomic_writers, cwlb_cost_params* out)
+{
+    return cwlb_calibrate_report(ctx, K, repeat, WI, load_MB, atomic_writers, out, nullptr);
 }
 
 cwlb_status cwlb_fill_features_uniform(cwlb_ctx* ctx, float* H, int64_t rows, int32_t K,

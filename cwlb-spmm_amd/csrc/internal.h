@@ -162,6 +162,7 @@ cwlb_status launch_reorder(cwlb_ctx* ctx, int32_t n_rows, int64_t nnz, const int
                            int32_t* row_ptr_out, int32_t* col_idx_out, float* val_out);
 
 cwlb_status run_calibration(cwlb_ctx* ctx, int32_t K, int32_t repeat, int32_t WI, int32_t load_MB,
-                            int32_t atomic_writers, cwlb_cost_params* out);
+                            int32_t atomic_writers, cwlb_cost_params* out,
+                            cwlb_calibration_report* report);
 
 }  // namespace cwlb

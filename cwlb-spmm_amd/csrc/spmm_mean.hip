@@ -816,21 +816,32 @@ struct Plan {
     const unsigned long long* hints;  // cold-column bits (device) or null
 };
 
+// Launches one instantiation; returns its resident waves per CU at most
+// (from its register and LDS use, queried once per instantiation).
 template <int VEC, int G, int R, int SL, bool HN = false, bool O6 = false>
-void launch_main(hipStream_t st, const SpmmArgs& a, const Plan& p, int* status)
+int launch_main(hipStream_t st, const SpmmArgs& a, const Plan& p, int* status)
 {
     constexpr int U = (R == 1) ? 8 : (R == 2) ? 4 : (R <= 4) ? 2 : 1;
+    static const int waves_per_cu = [] {
+        int blocks = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                &blocks, reinterpret_cast<const void*>(&spmm_mean_runs<VEC, G, R, U, SL, HN, O6>),
+                kBlock, 0) != hipSuccess)
+            blocks = 0;
+        return blocks * kWaves;
+    }();
     hipLaunchKernelGGL((spmm_mean_runs<VEC, G, R, U, SL, HN, O6>),
                        dim3(static_cast<unsigned>(p.grid)), dim3(kBlock), 0, st, a.row_ptr,
                        a.col_idx, a.val, a.origin, a.n_rows, static_cast<long long>(a.nnz), a.H,
                        static_cast<long long>(a.h_rows), a.K, a.tasks,
                        static_cast<long long>(a.n_tasks), p.M, p.runs, p.blocks, p.chunk, p.order,
                        p.hints, a.C, status);
+    return waves_per_cu;
 }
 
 // Feature slices of one lane group (one vector per lane) under cache hints.
 template <int VEC, int SL>
-void dispatch_hinted(hipStream_t st, const SpmmArgs& a, const Plan& p, int* status, int G)
+int dispatch_hinted(hipStream_t st, const SpmmArgs& a, const Plan& p, int* status, int G)
 {
     switch (G) {
     case 1: return launch_main<VEC, 1, 1, SL, true>(st, a, p, status);
@@ -845,7 +856,7 @@ void dispatch_hinted(hipStream_t st, const SpmmArgs& a, const Plan& p, int* stat
 
 // The occupancy variant: slots of 4, 8 or 16 lanes of 16 bytes.
 template <int SL, bool HN>
-void dispatch_o6(hipStream_t st, const SpmmArgs& a, const Plan& p, int* status, int G)
+int dispatch_o6(hipStream_t st, const SpmmArgs& a, const Plan& p, int* status, int G)
 {
     switch (G) {
     case 4: return launch_main<4, 4, 1, SL, HN, true>(st, a, p, status);
@@ -855,7 +866,7 @@ void dispatch_o6(hipStream_t st, const SpmmArgs& a, const Plan& p, int* status, 
 }
 
 template <int VEC, int SL>
-void dispatch_width(hipStream_t st, const SpmmArgs& a, const Plan& p, int* status)
+int dispatch_width(hipStream_t st, const SpmmArgs& a, const Plan& p, int* status)
 {
     const int F = a.K / SL / VEC;
     if (F <= 64) {
@@ -896,7 +907,7 @@ void dispatch_width(hipStream_t st, const SpmmArgs& a, const Plan& p, int* statu
 }
 
 template <int VEC>
-void dispatch_main(hipStream_t st, const SpmmArgs& a, const Plan& p, int* status)
+int dispatch_main(hipStream_t st, const SpmmArgs& a, const Plan& p, int* status)
 {
     if (p.sl == 8) return dispatch_width<VEC, 8>(st, a, p, status);
     if (p.sl == 4) return dispatch_width<VEC, 4>(st, a, p, status);
@@ -1038,6 +1049,7 @@ cwlb_status launch_spmm_mean(cwlb_ctx* ctx, const SpmmArgs& a, bool zero_all, bo
     ctx->last_launch.vector_width = p.vec;
     ctx->last_launch.waves_per_simd = p.o6 ? 6 : 0;
     ctx->last_launch.grid_blocks = a.n_tasks > 0 && a.K > 0 ? p.grid : 0;
+    ctx->last_launch.max_waves_per_cu = 0;
     if (!zero_all && a.n_tasks > 0 && a.K > 0) {
         if (p.vec == 4) launch_zero<4>(st, a, p, ctx->d_status);
         else if (p.vec == 2) launch_zero<2>(st, a, p, ctx->d_status);
@@ -1048,9 +1060,11 @@ cwlb_status launch_spmm_mean(cwlb_ctx* ctx, const SpmmArgs& a, bool zero_all, bo
     CWLB_HIP_TRY(hipGetLastError());
     if (record_events) CWLB_HIP_TRY(hipEventRecord(ctx->ev[1], st));
     if (a.n_tasks > 0 && a.K > 0) {
-        if (p.vec == 4) dispatch_main<4>(st, a, p, ctx->d_status);
-        else if (p.vec == 2) dispatch_main<2>(st, a, p, ctx->d_status);
-        else dispatch_main<1>(st, a, p, ctx->d_status);
+        int waves = 0;
+        if (p.vec == 4) waves = dispatch_main<4>(st, a, p, ctx->d_status);
+        else if (p.vec == 2) waves = dispatch_main<2>(st, a, p, ctx->d_status);
+        else waves = dispatch_main<1>(st, a, p, ctx->d_status);
+        ctx->last_launch.max_waves_per_cu = waves;
         CWLB_HIP_TRY(hipGetLastError());
     }
     if (record_events) CWLB_HIP_TRY(hipEventRecord(ctx->ev[2], st));

@@ -32,7 +32,8 @@ EXPORTS = [
     "cwlb_partition_device",
     "cwlb_capacity_from_s", "cwlb_wave_based_s", "cwlb_recommended_candidate_w",
     "cwlb_candidate_search_bounds", "cwlb_candidate_search_by_count",
-    "cwlb_candidate_search_by_step", "cwlb_calibrate", "cwlb_save_costs", "cwlb_read_costs",
+    "cwlb_candidate_search_by_step", "cwlb_calibrate", "cwlb_calibrate_report", "cwlb_save_costs",
+    "cwlb_read_costs",
     "cwlb_fill_features_uniform",
 ]
 
@@ -64,6 +65,13 @@ def costs(c4) -> CostParams:
     return p
 
 
+class CalibrationReport(C.Structure):
+    _fields_ = [("compute_ms", C.c_double), ("load_ms", C.c_double), ("store_ms", C.c_double),
+                ("atomic_ms", C.c_double), ("compute_ops", C.c_int64), ("load_ops", C.c_int64),
+                ("store_ops", C.c_int64), ("atomic_ops", C.c_int64), ("load_bytes", C.c_int64),
+                ("store_bytes", C.c_int64)]
+
+
 class Timing(C.Structure):
     _fields_ = [("zero_us", C.c_float), ("main_us", C.c_float), ("total_us", C.c_float)]
 
@@ -72,7 +80,7 @@ class LaunchInfo(C.Structure):
     _fields_ = [("tasks_per_wave", C.c_int32), ("feature_slices", C.c_int32),
                 ("run_order", C.c_int32), ("xcd_blocks", C.c_int32),
                 ("cache_hints", C.c_int32), ("vector_width", C.c_int32),
-                ("waves_per_simd", C.c_int32), ("reserved", C.c_int32),
+                ("waves_per_simd", C.c_int32), ("max_waves_per_cu", C.c_int32),
                 ("grid_blocks", C.c_int64)]
 
 
@@ -139,6 +147,8 @@ def lib():
         L.cwlb_candidate_search_by_count.argtypes = [i32, i32, i32, vp, i64, C.POINTER(i64)]
         L.cwlb_candidate_search_by_step.argtypes = [i32, i32, i32, vp, i64, C.POINTER(i64)]
         L.cwlb_calibrate.argtypes = [vp, i32, i32, i32, i32, i32, C.POINTER(CostParams)]
+        L.cwlb_calibrate_report.argtypes = [vp, i32, i32, i32, i32, i32, C.POINTER(CostParams),
+                                            C.POINTER(CalibrationReport)]
         L.cwlb_save_costs.argtypes = [C.POINTER(CostParams), C.c_char_p, C.c_int, C.c_int]
         L.cwlb_read_costs.argtypes = [C.POINTER(CostParams), C.c_char_p]
         L.cwlb_fill_features_uniform.argtypes = [vp, vp, i64, i32, u64]
@@ -397,6 +407,14 @@ class Context:
         check(lib().cwlb_calibrate(self.h, int(K), int(repeat), int(WI), int(load_MB),
                                    int(atomic_writers), C.byref(cp)))
         return cp
+
+    def calibrate_report(self, K=128, repeat=500, WI=131072, load_MB=512, atomic_writers=8):
+        """(CostParams, CalibrationReport): the coefficients and what each was
+        computed from (mean launch ms, operation count)."""
+        cp, rep = CostParams(), CalibrationReport()
+        check(lib().cwlb_calibrate_report(self.h, int(K), int(repeat), int(WI), int(load_MB),
+                                          int(atomic_writers), C.byref(cp), C.byref(rep)))
+        return cp, rep
 
     def fill_features(self, H, rows, K, seed=42):
         check(lib().cwlb_fill_features_uniform(self.h, _ptr(H), int(rows), int(K), int(seed)))

@@ -167,7 +167,8 @@ typedef struct cwlb_launch_info {
     int32_t cache_hints;     /* 1 when the gathers carried cache hints */
     int32_t vector_width;    /* floats per load: 4, 2 or 1 */
     int32_t waves_per_simd;  /* 6 for the occupancy variant, else 0 */
-    int32_t reserved;
+    int32_t max_waves_per_cu; /* resident waves per CU the kernel's register
+                                 and LDS use allow */
     int64_t grid_blocks;     /* work-groups of the aggregation kernel */
 } cwlb_launch_info;
 cwlb_status cwlb_ctx_last_launch(cwlb_ctx* ctx, cwlb_launch_info* out);
@@ -385,6 +386,33 @@ cwlb_status cwlb_candidate_search_by_step(int32_t lower, int32_t upper, int32_t 
  * Fills out->K, WI, repeat and atomic_writers_per_addr too. */
 cwlb_status cwlb_calibrate(cwlb_ctx* ctx, int32_t K, int32_t repeat, int32_t WI,
                            int32_t load_MB, int32_t atomic_writers, cwlb_cost_params* out);
+
+/* What each coefficient of a calibration was computed from: the mean
+ * event-timed launch duration of its micro-benchmark (ms) and the operation
+ * count it is divided by.  coefficient = ms * 1e6 / ops * 10, with ops =
+ * WI * K for compute, load and store (utils.cpp:419-421, 522-524, 583-585)
+ * and ops = writer groups * feature block for the atomic (:791-806).
+ * bytes_* are the bytes one launch of the load / store benchmark reads /
+ * writes through its loads and stores (4 per op). */
+typedef struct cwlb_calibration_report {
+    double compute_ms;
+    double load_ms;
+    double store_ms;
+    double atomic_ms;
+    int64_t compute_ops;
+    int64_t load_ops;
+    int64_t store_ops;
+    int64_t atomic_ops;
+    int64_t load_bytes;
+    int64_t store_bytes;
+} cwlb_calibration_report;
+
+/* cwlb_calibrate that also fills *report (may be NULL).  No counterpart in
+ * the reference, which prints these figures (utils.cpp:806-825); tests use
+ * it to check the normalisation. */
+cwlb_status cwlb_calibrate_report(cwlb_ctx* ctx, int32_t K, int32_t repeat, int32_t WI,
+                                  int32_t load_MB, int32_t atomic_writers, cwlb_cost_params* out,
+                                  cwlb_calibration_report* report);
 
 /* Cost file (utils.cpp:1024-1092): four lines compute/load/store/atomic,
  * fixed notation with `precision` decimals; the parent directory is

@@ -55,6 +55,9 @@ def lib():
         L.oracle_spmm_mean_f32_omp.argtypes = [C.c_int, i32p, i32p, f32p, i32p, f32p, C.c_int,
                                                i32p, C.c_long, f32p, C.c_int]
         L.oracle_max_threads.restype = C.c_int
+        L.oracle_cost_coefficients.argtypes = [f64p, C.c_int, C.c_int, C.c_int, f64p,
+                                               np.ctypeslib.ndpointer(dtype=np.int64,
+                                                                      flags="C_CONTIGUOUS")]
         L.oracle_format_costs.argtypes = [f64p, C.c_int, C.c_char_p, C.c_long]
         L.oracle_format_costs.restype = C.c_int
         L.oracle_parse_costs.argtypes = [C.c_char_p, f64p]
@@ -223,6 +226,15 @@ def spmm_mean_f64(rp, ci, val, H):
     out = np.zeros((n, K), np.float64)
     lib().oracle_spmm_mean_f64(n, _i32(rp), _i32(ci), _f32(val), H.reshape(-1), K, out.reshape(-1))
     return out
+
+
+def cost_coefficients(ms4, K, WI, writers):
+    """utils.cpp:419-421, 522-524, 583-585, 791-806 -> (coefficients[4], ops[4])."""
+    out = np.zeros(4, np.float64)
+    ops = np.zeros(4, np.int64)
+    lib().oracle_cost_coefficients(np.ascontiguousarray(ms4, np.float64), int(K), int(WI),
+                                   int(writers), out, ops)
+    return [float(x) for x in out], [int(x) for x in ops]
 
 
 def max_threads():

@@ -28,7 +28,8 @@
  * catch it (0 = faithful restatement).  1: next-row prefix absorption
  * disabled; 2: current-row prefix absorption disabled; 3: strict '<' in the
  * packing rule; 4: divide by chunk length instead of full degree;
- * 5: reorder ties broken by descending id. */
+ * 5: reorder ties broken by descending id; 7: atomic calibration divides
+ * by the group target instead of the rounded-up writer groups. */
 static int g_mutation = 0;
 void oracle_set_mutation(int m) { g_mutation = m; }
 
@@ -541,6 +542,44 @@ int oracle_max_threads(void)
 #else
     return 1;
 #endif
+}
+
+/* ------------------------------------------------------------------------
+ * Calibration normalisation: utils.cpp:419-421 (compute), 522-524 (load),
+ * 583-585 (store): C = ((mean_ms * 1e6) / WI) / K * 10, i.e. ns per op per
+ * work-item x 10; utils.cpp:597-640 and 791-806 (atomic): K_block =
+ * min(K, 128) rounded down to a multiple of 32 (32 when that is 0), writer
+ * groups = the smallest multiple of `writers` (>= 1) that reaches
+ * ceil(WI / 128) (at least `writers`), ops = groups * K_block,
+ * C_atomic = (mean_ms * 1e6) / ops * 10.  ms[] = compute, load, store,
+ * atomic mean launch times; out[] the four coefficients; ops[] the divisors.
+ * Pinned by hand-derived known answers in tests (exact binary fractions).
+ * ---------------------------------------------------------------------- */
+void oracle_cost_coefficients(const double *ms, int K, int WI, int writers,
+                              double *out, long long *ops)
+{
+    for (int i = 0; i < 3; ++i) {
+        double per_wi = (ms[i] * 1e6) / (double)WI;
+        out[i] = per_wi / (double)K * 10;
+        ops[i] = (long long)WI * K;
+    }
+    int gpr = writers > 1 ? writers : 1;
+    int kb = K < 128 ? K : 128;
+    kb = (kb / 32) * 32;
+    if (kb <= 0) kb = 32;
+    int target = (WI + 127) / 128;
+    if (target < 1) target = 1;
+    int G = target / gpr;
+    if (G < 1) G = 1;
+    long long groups = (long long)G * gpr;
+    while (groups < target) {
+        ++G;
+        groups = (long long)G * gpr;
+    }
+    if (g_mutation == 7) groups = target;
+    double n_ops = (double)groups * (double)kb;
+    out[3] = (ms[3] * 1.0e6) / n_ops * 10.0;
+    ops[3] = groups * kb;
 }
 
 /* ------------------------------------------------------------------------

@@ -1,8 +1,9 @@
-"""bench.py's host-side helpers (no GPU): the measured-traffic lookup reads
-the committed rocprofv3 summaries by segment size, and the algorithmic-bytes
-formula matches its per-unit statement."""
+"""bench.py's host-side helpers (no GPU): the roofline record computed from
+counter values, the counter CSV reader, the launch arguments handed to the
+counter passes, and the algorithmic / compulsory byte formulas."""
 import importlib
 import os
+import subprocess
 import sys
 
 import pytest
@@ -16,33 +17,77 @@ def bench():
     return importlib.import_module("bench")
 
 
-# The S values the summaries were measured at (the three wave-based
-# candidates of each workload with 256 CUs).
-MEASURED = {4: (32, 63, 125), 5: (39, 77, 153), 2: (35, 70, 139), 3: (55, 110, 220)}
+KERNEL = ("void cwlb::(anonymous namespace)::spmm_mean_runs<4, 16, 1, 8, 2, true, false>"
+          "(int const*, int const*, float const*, int const*, int, long long, ...)")
 
 
-@pytest.mark.parametrize("cfg", sorted(MEASURED))
-def test_traffic_figure_per_candidate_s(bench, cfg):
-    for S in MEASURED[cfg]:
-        t = bench.measured_traffic(cfg, S)
-        assert t is not None and t > 0, (cfg, S)
+def counters(fetch_kib, write_kib, probe_fetch_kib, probe_write_kib, hits=1.0, misses=3.0,
+             occ=17.5):
+    return {"kernel": {"FETCH_SIZE": fetch_kib, "WRITE_SIZE": write_kib, "TCC_HIT_sum": hits,
+                       "TCC_MISS_sum": misses, "MeanOccupancyPerCU": occ},
+            "copy": {"FETCH_SIZE": probe_fetch_kib, "WRITE_SIZE": probe_write_kib},
+            "name": KERNEL, "dispatches": 4}
 
 
-def test_traffic_unknown_s_or_workload_is_none(bench):
-    assert bench.measured_traffic(4, 64) is None
-    assert bench.measured_traffic(3, 56) is None
-    assert bench.measured_traffic(1, 9) is None  # no summary for the small ER graph
+def test_roofline_from_counters(bench):
+    """frac = (FETCH x read scale + WRITE x write scale) / kernel time / 8 TB/s,
+    with the scales from the 1 GiB copy; the algorithmic and compulsory
+    rates beside it; a 4 ms launch moving 24 GB runs at 6 TB/s = 0.75."""
+    probe_kib = 1 << 20  # 1 GiB
+    # FETCH_SIZE reads half of the copy's bytes: read scale 2; WRITE exact.
+    c = counters(fetch_kib=10e9 / 1024 / 2, write_kib=14e9 / 1024, probe_fetch_kib=probe_kib / 2,
+                 probe_write_kib=probe_kib)
+    rec = bench.roofline_record(c, None, b_alg=36e9, b_min=4.8e9, main_us=4000.0,
+                                launched={"max_waves_per_cu": 28})
+    assert rec["traffic"] == pytest.approx(24e9)
+    assert rec["traffic_read"] == pytest.approx(10e9) and rec["traffic_write"] == pytest.approx(14e9)
+    assert rec["achieved"] == pytest.approx(6000.0) and rec["frac"] == pytest.approx(0.75)
+    assert rec["frac"] == pytest.approx(rec["traffic"] / (rec["kernel_us"] * 1e-6) / 8e12)
+    assert rec["effective_gbs"] == pytest.approx(9000.0)
+    assert rec["compulsory_gbs"] == pytest.approx(1200.0)
+    assert rec["compulsory_frac"] == pytest.approx(0.15)
+    assert rec["l2_hit_rate"] == pytest.approx(0.25)
+    assert rec["waves_per_cu"] == 17.5 and rec["max_waves_per_cu"] == 28
+    assert rec["kernel"] == "spmm_mean_runs<4,16,1,8,2,true,false>"
+    assert rec["counters"]["fetch_scale"] == pytest.approx(2.0)
+    assert (rec["bound"], rec["unit"], rec["peak"]) == ("hbm", "GB/s", 8000.0)
 
 
-def test_traffic_figures_are_consistent_with_algorithmic_bytes(bench):
-    """Measured traffic below the algorithmic bytes where caches serve
-    repeated feature rows (R-MAT, Chung-Lu, mesh), and within a few percent
-    above it where every gather misses and rows straddle cache lines (SBM)."""
-    from cwlb_amd import workloads
-    ratios = {4: (63, 4194304, 65245138, 128, 1084009), 3: (55, 240000, 115180734, 600, 2217632)}
-    for cfg, (S, n, nnz, K, T) in ratios.items():
-        r = bench.measured_traffic(cfg, S) / workloads.algorithmic_bytes(n, nnz, K, T)
-        assert (0.5 < r < 1.0) if cfg == 4 else (1.0 < r < 1.05), (cfg, r)
+def test_roofline_without_counters(bench):
+    rec = bench.roofline_record(None, "rocprofv3 not found", 36e9, 4.8e9, 4000.0, {})
+    assert rec["traffic"] is None and rec["frac"] is None and rec["achieved"] is None
+    assert rec["counters_error"] == "rocprofv3 not found"
+    assert rec["effective_gbs"] == pytest.approx(9000.0)
+
+
+def test_counter_csv_reader(bench, tmp_path):
+    """Rows grouped per (kernel, counter) in dispatch order."""
+    path = tmp_path / "run_counter_collection.csv"
+    path.write_text(
+        "Correlation_Id,Dispatch_Id,Agent_Id,Queue_Id,Process_Id,Thread_Id,Grid_Size,Kernel_Id,"
+        "Kernel_Name,Workgroup_Size,LDS_Block_Size,Scratch_Size,VGPR_Count,Accum_VGPR_Count,"
+        "SGPR_Count,Counter_Name,Counter_Value,Start_Timestamp,End_Timestamp\n"
+        f'3,3,1,1,9,9,4096,7,"{KERNEL}",256,0,0,72,0,96,FETCH_SIZE,30.0,0,1\n'
+        f'1,1,1,1,9,9,4096,7,"{KERNEL}",256,0,0,72,0,96,FETCH_SIZE,10.0,0,1\n'
+        '2,2,1,1,9,9,4096,8,"__amd_rocclr_copyBuffer",256,0,0,8,0,16,FETCH_SIZE,5.0,0,1\n'
+        '4,4,1,1,9,9,4096,8,"__amd_rocclr_copyBuffer",256,0,0,8,0,16,FETCH_SIZE,7.0,0,1\n')
+    vals = bench.read_counter_csv(str(path))
+    assert vals[(KERNEL, "FETCH_SIZE")] == [10.0, 30.0]
+    assert vals[("__amd_rocclr_copyBuffer", "FETCH_SIZE")] == [5.0, 7.0]
+
+
+def test_schedule_args_fix_the_launch(bench):
+    sched = {"tasks_per_wave": 64, "feature_slices": 2, "run_order": 0, "xcd_blocks": 0,
+             "hot_bytes": 48 << 20, "occupancy": 0}
+    args = bench.schedule_args(63, sched)
+    assert args == ["--s", "63", "--tasks-per-wave", "64", "--slices", "2", "--run-order", "0",
+                    "--xcd-blocks", "0", "--hot-mb", "48", "--occupancy", "0"]
+
+
+def test_more_than_one_gpu_is_refused():
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"],
+                       capture_output=True, text=True)
+    assert r.returncode == 2 and "one GPU only" in r.stderr
 
 
 def test_algorithmic_bytes_formula():
@@ -54,3 +99,13 @@ def test_algorithmic_bytes_formula():
     assert workloads.algorithmic_bytes(n, nnz, K, T) == (
         4 * (n + 1) + 8 * nnz + 4 * nnz * K + 4 * n * K + 4 * n + 16 * T)
     assert workloads.algorithmic_bytes(4194304, 65245138, 128, 1084009) == 36125853988
+
+
+def test_compulsory_bytes_formula():
+    """CSR once, each referenced feature row once, C once: the R-MAT bound
+    with every row referenced is the 4.85 GB of the baseline table."""
+    from cwlb_amd import workloads
+    n, nnz, K = 4194304, 65245138, 128
+    b = workloads.compulsory_bytes(n, n, nnz, K)
+    assert b == 4 * (n + 1) + 8 * nnz + 4 * n * K + 4 * n * K + 4 * n
+    assert 4.8e9 < b < 4.9e9

@@ -99,7 +99,36 @@ def test_device_reorder_rejects_bad_offsets(gpu_ctx):
 
 
 # ------------------------------------------------------------- calibration
-def test_calibration_small(gpu_ctx):
+@pytest.mark.parametrize("K,WI,writers", [(128, 131072, 8), (64, 8192, 8), (40, 1000, 3)])
+def test_calibration_normalisation(gpu_ctx, K, WI, writers):
+    """Each coefficient is the reference's normalisation of its benchmark's
+    measured mean launch time: (ms * 1e6) / WI / K * 10 for compute, load
+    and store, (ms * 1e6) / ops * 10 for the atomic with ops = writer groups
+    x feature block (utils.cpp:419-421, 522-524, 583-585, 791-806), equal
+    bit for bit to the oracle's restatement applied to the reported times.
+    The times obey the hardware's limits: the stores and loads move at most
+    8 TB/s (40 bytes / coefficient per ns), the fma chains run below the
+    157.3 TFLOP/s FP32 peak, and a contended atomic costs more than a
+    coalesced store (the default shapes, the costWrite defaults with fewer
+    repeats)."""
+    c, rep = gpu_ctx.calibrate_report(K=K, repeat=20, WI=WI, load_MB=64, atomic_writers=writers)
+    ms = (rep.compute_ms, rep.load_ms, rep.store_ms, rep.atomic_ms)
+    assert all(np.isfinite(ms)) and all(m > 0 for m in ms), ms
+    want, ops = oracle.cost_coefficients(ms, K, WI, writers)
+    assert list(c.tuple4()) == want, (c.tuple4(), want)
+    assert [rep.compute_ops, rep.load_ops, rep.store_ops, rep.atomic_ops] == ops
+    assert rep.load_bytes == rep.store_bytes == 4 * WI * K
+    assert (c.K, c.WI, c.repeat, c.atomic_writers_per_addr) == (K, WI, 20, writers)
+    if K == 128:
+        store_gbs, load_gbs = 40.0 / c.C_store_ns, 40.0 / c.C_load_ns
+        assert store_gbs == pytest.approx(rep.store_bytes / (rep.store_ms * 1e6), rel=1e-12)
+        assert store_gbs <= 8000.0 and load_gbs <= 8000.0, (store_gbs, load_gbs)
+        assert 2.0 * WI * K / (rep.compute_ms * 1e-3) <= 157.3e12
+        assert c.C_atomic_ns > c.C_store_ns, c.tuple4()
+    print(f"K={K} WI={WI}: coefficients {c.tuple4()} from ms {ms}", flush=True)
+
+
+def test_calibration_arguments(gpu_ctx):
     c = gpu_ctx.calibrate(K=64, repeat=3, WI=8192, load_MB=16, atomic_writers=8)
     vals = c.tuple4()
     assert all(np.isfinite(vals)) and all(v > 0 for v in vals), vals

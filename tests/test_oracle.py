@@ -383,3 +383,44 @@ def test_planted_reorder_mistake_is_caught():
     finally:
         oracle.set_mutation(0)
     assert not np.array_equal(origin, np.argsort(np.diff(g.row_ptr), kind="stable"))
+
+
+# ------------------------------------------------- calibration normalisation
+# Hand-derived from utils.cpp:419-421, 522-524, 583-585 (ns per op per
+# work-item x 10) and 597-640, 791-806 (atomic: writer groups rounded up to a
+# multiple of the writers per address, ops = groups x K_block).  The inputs
+# are chosen so that every coefficient is an exact binary fraction.
+CAL_KATS = [
+    # ms (compute, load, store, atomic), K, WI, writers -> ops, coefficients
+    ((1.0, 2.0, 0.5, 4.0), 128, 131072, 8,
+     (16777216, 16777216, 16777216, 131072),   # 1024 groups x K_block 128
+     (78125 / 2**17, 2 * 78125 / 2**17, 78125 / 2**18, 305.17578125)),
+    # K = 40: K_block 32; ceil(1000 / 128) = 8 groups wanted, 8 // 3 = 2
+    # rows give 6 < 8, so 3 rows of 3 writers: 9 groups, 288 atomics.
+    ((0.25, 0.25, 0.25, 0.0288), 40, 1000, 3,
+     (40000, 40000, 40000, 288),
+     (0.25e6 / 1000 / 40 * 10,) * 3 + (1000.0,)),
+    # K = 20 rounds K_block down to 0, which becomes 32; 1 writer.
+    ((0.5, 0.5, 0.5, 0.5), 20, 64, 1,
+     (1280, 1280, 1280, 32), (0.5e6 / 64 / 20 * 10,) * 3 + (0.5e6 / 32 * 10,)),
+]
+
+
+@pytest.mark.parametrize("case", range(len(CAL_KATS)))
+def test_calibration_normalisation_known_answers(case):
+    ms, K, WI, writers, ops, coef = CAL_KATS[case]
+    got, got_ops = oracle.cost_coefficients(ms, K, WI, writers)
+    assert got_ops == list(ops)
+    assert got == pytest.approx(list(coef), rel=1e-15)
+    if case == 0:
+        assert got == list(coef)  # exact binary fractions
+
+
+def test_planted_calibration_mistake_is_caught():
+    ms, K, WI, writers, ops, coef = CAL_KATS[1]
+    try:
+        oracle.set_mutation(7)
+        got, got_ops = oracle.cost_coefficients(ms, K, WI, writers)
+    finally:
+        oracle.set_mutation(0)
+    assert got_ops[3] != ops[3] and got[3] != pytest.approx(coef[3])
