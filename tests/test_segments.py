@@ -82,32 +82,30 @@ def cleared_rows(rp, origin, tasks, M, n_rows, nnz):
     rows = set()
     for base in range(0, T, 64):  # one 64-lane wave
         lanes = range(base, min(base + 64, T))
-        brk, ends, o1, o2 = [True] * 64, [False] * 64, [-1] * 64, [-1] * 64
+        brk, ends, o = [True] * 64, [False] * 64, [-1] * 64
         for t in lanes:
             i = t - base
             cur = tasks[t]
             prev = tasks[t - 1] if t > 0 else cur
             brk[i] = segment_break(prev, cur, t % M, n_rows)
-            rlo, rhi = max(int(cur[0]), 0), min(int(cur[1]), n_rows)
-            if rlo < rhi:
-                _, b, e, d = row_chunk(rp, rlo, cur, nnz)
-                ends[i] = e == d
-                open_a = d > 0 and b == 0 and 0 < e < d
-                if rhi - 1 == rlo:
-                    if open_a:
-                        o2[i] = origin[rlo]
-                else:
-                    if open_a:
-                        o1[i] = origin[rlo]
-                    _, b, e, d = row_chunk(rp, rhi - 1, cur, nnz)
-                    if d > 0 and b == 0 and 0 < e < d:
-                        o2[i] = origin[rhi - 1]
+            rs, re, fo, ln = (int(x) for x in cur)
+            r = -1
+            if well_formed(cur, n_rows):
+                ends[i] = re - rs > 1 or ln == 0
+                if ln > 0 and (re - rs > 1 or fo == 0):
+                    r = re - 1
+            elif max(rs, 0) < min(re, n_rows):
+                r = min(re, n_rows) - 1
+            if r >= 0:
+                _, b, e, d = row_chunk(rp, r, cur, nnz)
+                if d > 0 and b == 0 and 0 < e < d:
+                    o[i] = origin[r]
         for i in range(64):
-            if o2[i] >= 0 and i < 63:
+            if o[i] >= 0 and i < 63:
                 ahead = [u for u in range(i + 1, 64) if brk[u] or ends[u]]
                 if ahead and not brk[ahead[0]]:
-                    o2[i] = -1  # completed inside the segment
-        rows.update(int(o) for o in o1 + o2 if 0 <= o < n_rows)
+                    o[i] = -1  # completed inside the segment
+        rows.update(int(x) for x in o if 0 <= x < n_rows)
     return rows
 
 
@@ -282,3 +280,28 @@ def test_emulation_catches_planted_mistakes(monkeypatch):
                   rng)
     assert np.isnan(got).any() and real_ballot is not None
     assert not np.allclose(np.nan_to_num(got), ref_tiled)
+
+
+def test_one_row_task_past_the_row_end():
+    """A one-row task whose end offset passes the row's degree is not
+    counted as ending the row by the look-ahead (the clearing pass then
+    clears a row that the segment later stores whole): the result is
+    still the reference's, with and without a following segment break."""
+    rp = np.array([0, 5, 9, 12], np.int32)
+    ci = np.array([0, 1, 2, 1, 0, 2, 2, 1, 0, 1, 0, 2], np.int32)
+    val = np.linspace(0.5, 2.0, 12).astype(np.float32)
+    origin = np.array([2, 0, 1], np.int32)
+    H = np.arange(6, dtype=np.float64).reshape(3, 2)
+    p = workloads.Prepared(3, 12, origin, rp, ci, val, None, 2, 0.0)
+    # (list, whether row 0 -- original id 2 -- is cleared)
+    lists = [
+        # the next task does not continue at offset 10: a segment break, so
+        # the look-ahead clears row 0, which the segment then stores whole
+        (np.array([[0, 1, 0, 3], [0, 1, 3, 10], [1, 3, 0, 0]], np.int32), True),
+        # the segment goes on into a task with more rows: row 0 complete
+        (np.array([[0, 1, 0, 3], [0, 1, 3, 10], [0, 2, 10, 0], [2, 3, 0, 0]], np.int32), False),
+    ]
+    for t, cleared in lists:
+        assert (2 in cleared_rows(rp, origin, t, 64, 3, 12)) == cleared
+        p.tasks = t
+        check_list(p, H, t, 64, zero_output=False, rng=np.random.default_rng(1))
