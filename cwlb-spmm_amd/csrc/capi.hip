@@ -448,8 +448,8 @@ cwlb_status cwlb_ctx_tune_schedule(cwlb_ctx* ctx, const int32_t* row_ptr, const 
     // Candidates: the automatic choice, then every run length and slice
     // count the kernel takes for this K.
     std::vector<std::pair<int, int>> cands{{0, 0}};
-    for (int sl : {1, 2, 4})
-        if (sl == 1 || (K % (4 * sl) == 0 && K / sl >= 32))
+    for (int sl : {1, 2, 4, 8})
+        if (sl == 1 || (K % 4 == 0 && K / sl >= 32))
             for (int m : {2, 4, 8, 16, 32, 64}) cands.emplace_back(m, sl);
     const int keep_m = ctx->sched_tasks_per_wave, keep_sl = ctx->sched_slices;
     // Tuning the hints and the occupancy variant too: the schedule and

@@ -361,16 +361,19 @@ spmm_mean_runs(const int* __restrict__ rp, const int* __restrict__ ci,
     // that order instead of task order.
     const long long run = run_order ? static_cast<long long>(run_order[pos]) : pos;
 
-    const int K = ld / SL;                       // features of this slice
-    const float* __restrict__ Hs = H + slice * K;
-    float* __restrict__ Cs = C + slice * K;
-    const int F = K / VEC;
+    // This slice's vectors [f0, f0 + F) of the row's ld / VEC: whole
+    // vectors, as even as the row allows (sizes differ by at most one).
+    const int FT = ld / VEC;
+    const int f0 = slice * FT / SL;
+    const int F = (slice + 1) * FT / SL - f0;
+    const float* __restrict__ Hs = H + f0 * VEC;
+    float* __restrict__ Cs = C + f0 * VEC;
     const int npass = (F + G * R - 1) / (G * R);
     int bad = 0;
     // Hinted gathers: byte offset of feature vector f of column c's slice.
     __amdgpu_buffer_rsrc_t hrsrc;
     if constexpr (HN) hrsrc = feature_rsrc(H, h_rows, ld);
-    const unsigned slice_bytes = static_cast<unsigned>(slice * K) * 4u;
+    const unsigned slice_bytes = static_cast<unsigned>(f0 * VEC) * 4u;
 
     // One segment: task (rs, re, fo, ln).
     auto run_segment = [&](const int rs, const int re, const int fo, const int ln) {
@@ -877,7 +880,7 @@ int dispatch_o6(hipStream_t st, const SpmmArgs& a, const Plan& p, int* status, i
 template <int VEC, int SL>
 int dispatch_width(hipStream_t st, const SpmmArgs& a, const Plan& p, int* status)
 {
-    const int F = a.K / SL / VEC;
+    const int F = (a.K / VEC + SL - 1) / SL;  // vectors of the widest slice
     if (F <= 64) {
         int G = 1;
         while (G < F) G <<= 1;
@@ -969,7 +972,7 @@ Plan make_plan(const cwlb_ctx* ctx, const SpmmArgs& a, bool per_task)
             if (a.K % 64 == 0 && a.K >= 64 && a.K <= 256) p.sl = 2;
             else if (a.K % 128 == 0 && a.K > 256 && a.K <= 512) p.sl = 4;
         }
-        if (p.vec != 4 || a.K % (4 * p.sl) != 0) p.sl = 1;
+        if (p.vec != 4 || a.K / 4 < p.sl) p.sl = 1;
         if (ctx->sched_tasks_per_wave > 0) {
             p.M = ctx->sched_tasks_per_wave;
         } else {
@@ -998,9 +1001,8 @@ Plan make_plan(const cwlb_ctx* ctx, const SpmmArgs& a, bool per_task)
     p.ordered = !per_task && ctx->sched_order == 2 && p.runs > 1;
     // The occupancy variant exists for 16-byte lanes and slots of 4 to 16
     // lanes (more than 8 and at most 64 floats per feature slice).
-    const int f4 = a.K / p.sl / 4;
-    p.o6 = !per_task && ctx->sched_occupancy == 6 && p.vec == 4 && a.K % (4 * p.sl) == 0 &&
-           f4 > 2 && f4 <= 16;
+    const int f4 = (a.K / 4 + p.sl - 1) / p.sl;  // vectors of the widest slice
+    p.o6 = !per_task && ctx->sched_occupancy == 6 && p.vec == 4 && f4 > 2 && f4 <= 16;
     p.order = nullptr;
     p.hints = nullptr;
     return p;
@@ -1030,7 +1032,7 @@ cwlb_status launch_spmm_mean(cwlb_ctx* ctx, const SpmmArgs& a, bool zero_all, bo
     // Cache hints: 16-byte lanes, one vector per lane and slice, and the
     // feature matrix addressable by 32-bit byte offsets.
     if (!per_task && ctx->sched_hot_bytes > 0 && p.vec == 4 && a.n_tasks > 0 && a.K > 0 &&
-        a.K / p.sl <= 256 &&
+        (a.K / 4 + p.sl - 1) / p.sl <= 64 &&
         static_cast<unsigned long long>(a.h_rows) * a.K * 4ull <= 0xFFFFFFFFull) {
         const long long hot_rows = ctx->sched_hot_bytes / (4ll * a.K);
         const cwlb_status s = build_cache_hints(ctx, a, hot_rows, may_build, &p.hints);

@@ -105,9 +105,10 @@ cwlb_status cwlb_ctx_device_info(cwlb_ctx* ctx, cwlb_device_info* out);
 /* Schedule of later SpMM calls on this context: tasks executed per wave
  * (a run of consecutive tasks) and feature slices spread across the XCDs.
  * 0 selects automatically (the default).  feature_slices must be 0, 1, 2, 4
- * or 8; a slice count that does not split K into multiples of 4 floats (or
- * with misaligned H / C) falls back to 1.  CWLB_SPMM_PER_TASK overrides both
- * with 1.  No counterpart in the reference (its work-group per task is
+ * or 8; the slices are whole 4-float vectors, as even as K allows (K = 600
+ * in 4 slices: 38, 38, 37 and 37 vectors).  K not a multiple of 4, fewer
+ * vectors than slices, or misaligned H / C fall back to 1 slice.
+ * CWLB_SPMM_PER_TASK overrides both with 1.  No counterpart in the reference (its work-group per task is
  * fixed); tuning and tests use it. */
 cwlb_status cwlb_ctx_set_schedule(cwlb_ctx* ctx, int32_t tasks_per_wave, int32_t feature_slices);
 
@@ -244,9 +245,10 @@ cwlb_status cwlb_spmm_mean_f32_large_k(cwlb_ctx* ctx, const int32_t* row_ptr,
                                        uint32_t flags, cwlb_timing* timing);
 
 /* Times the aggregation of these (device) inputs under the automatic
- * schedule and under every tasks-per-wave value in {2, 4, ..., 64} with 1, 2
- * or 4 feature slices (where K allows them), `trials` event-timed calls each
- * after one warm-up (median of split-row clearing + aggregation), and sets
+ * schedule and under every tasks-per-wave value in {2, 4, ..., 64} with 1,
+ * 2, 4 or 8 feature slices (slices of at least 32 floats), `trials`
+ * event-timed calls each after one warm-up (median of split-row clearing +
+ * aggregation), and sets
  * the fastest on the context (cwlb_ctx_set_schedule); the choice is also
  * returned through the optional out pointers (0, 0 = the automatic schedule
  * won).  With locality_out non-null (two int32), the fastest schedule is
