@@ -474,11 +474,12 @@ def test_many_per_row_tasks_in_any_order(gpu_ctx, order):
 
 
 @pytest.mark.parametrize("how", ["shuffled", "swapped_pairs", "gaps"])
-@pytest.mark.parametrize("m", [0, 64, 5])
+@pytest.mark.parametrize("m", [0, 64, 5, 130])
 def test_partition_list_out_of_order(gpu_ctx, how, m):
     """The partition's task list (split rows included) shuffled, with pairs
     of neighbours swapped, or with a fifth of the tasks dropped, at the
-    automatic run length and at 64 and 5 tasks per wave: with the full clear
+    automatic run length and at 64, 5 and 130 tasks per wave (a run of
+    three 64-task windows): with the full clear
     of CWLB_SPMM_ZERO_OUTPUT the result is the reference's for that list."""
     rng = np.random.default_rng(len(how) + m)
     g = workloads.small(4, seed=23)

@@ -94,3 +94,28 @@ def test_noalloc_large_k_and_errors(gpu_ctx):
             capi.spmm_noalloc(stream, d[0], d[1], d[2], d[3], g.n, g.nnz, d_H, g.n, 1100, d_t,
                               len(p.tasks), C, **kw)
         assert e.value.status == capi.INVALID_ARG
+
+
+def test_noalloc_captured_into_a_graph(gpu_ctx):
+    """The allocation-free call captured into a HIP graph and replayed, with
+    eager work between the replays, gives the context entry's result on
+    every replay."""
+    import torch
+    g, p, H, d, d_H, d_t = _inputs(torch, 4, 33, 64, 7, SKEWED_COSTS)
+    _, want = _both(gpu_ctx, torch, g, p, d, d_H, d_t, 64)
+    C = torch.zeros((g.n, 64), dtype=torch.float32, device="cuda")
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            capi.spmm_noalloc(side.cuda_stream, d[0], d[1], d[2], d[3], g.n, g.nnz, d_H, g.n,
+                              64, d_t, len(p.tasks), C, synchronize=False)
+    torch.cuda.synchronize()
+    for i in range(3):
+        C.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        np.testing.assert_allclose(C.cpu().numpy(), want, rtol=RTOL, atol=ATOL)
+        _ = (d_H * 2.0).sum().item()  # eager work between replays
