@@ -5,7 +5,11 @@
 // load the rows of the other, "cold" columns with the non-temporal policy,
 // so that they do not push the hot rows out of L2 and the Infinity Cache.
 // The hint is one bit per nonzero (1 = cold column), built on the device:
-//   1. column_counts: the in-degree of every column;
+//   1. column_counts: the in-degree of every column, counted on every
+//      stride-th nonzero (stride = 1 up to kSampleTarget nonzeros, then
+//      the smallest stride that keeps about kSampleTarget of them: a
+//      sample keeps the order of the large in-degrees that decide the hot
+//      set, at a fraction of the contended atomics);
 //   2. count_buckets: a histogram of the in-degrees over kBuckets
 //      log-spaced buckets (exact below 64, then 8 buckets per octave);
 //   3. on the host, the in-degree threshold theta: the lowest bucket floor
@@ -27,6 +31,7 @@ namespace cwlb {
 namespace {
 
 constexpr int kBlock = 256;
+constexpr long long kSampleTarget = 8ll << 20;  // in-degree samples at most (about)
 constexpr int kBuckets = 64 + 26 * 8;  // exact 0..63, then 8 per octave up to 2^32
 
 __device__ __forceinline__ int bucket_of(unsigned v)
@@ -55,13 +60,14 @@ __global__ void __launch_bounds__(kBlock) zero_u32(unsigned* __restrict__ p, lon
 }
 
 __global__ void __launch_bounds__(kBlock)
-column_counts(const int* __restrict__ ci, long long nnz, long long h_rows,
+column_counts(const int* __restrict__ ci, long long nnz, long long h_rows, long long sample,
               unsigned* __restrict__ counts)
 {
+    const long long n = (nnz + sample - 1) / sample;
     const long long stride = static_cast<long long>(gridDim.x) * kBlock;
-    for (long long j = static_cast<long long>(blockIdx.x) * kBlock + threadIdx.x; j < nnz;
-         j += stride) {
-        const int c = ci[j];
+    for (long long i = static_cast<long long>(blockIdx.x) * kBlock + threadIdx.x; i < n;
+         i += stride) {
+        const int c = ci[i * sample];
         if (c >= 0 && c < h_rows) atomicAdd(counts + c, 1u);
     }
 }
@@ -148,9 +154,10 @@ cwlb_status build_cache_hints(cwlb_ctx* ctx, const SpmmArgs& a, long long hot_ro
     hipLaunchKernelGGL(zero_u32, dim3(1), dim3(kBlock), 0, st, ctx->d_count_hist,
                        static_cast<long long>(kBuckets));
     CWLB_LAUNCH_CHECK("zero_u32");
-    hipLaunchKernelGGL(column_counts, dim3(grid_for(a.nnz)), dim3(kBlock), 0, st, a.col_idx,
-                       static_cast<long long>(a.nnz), static_cast<long long>(a.h_rows),
-                       ctx->d_col_counts);
+    const long long sample = std::max(1ll, static_cast<long long>(a.nnz) / kSampleTarget);
+    hipLaunchKernelGGL(column_counts, dim3(grid_for(a.nnz / sample)), dim3(kBlock), 0, st,
+                       a.col_idx, static_cast<long long>(a.nnz), static_cast<long long>(a.h_rows),
+                       sample, ctx->d_col_counts);
     CWLB_LAUNCH_CHECK("column_counts");
     hipLaunchKernelGGL(count_buckets, dim3(std::min(grid_for(a.h_rows), 1024u)), dim3(kBlock), 0,
                        st, ctx->d_col_counts, static_cast<long long>(a.h_rows), ctx->d_count_hist);
@@ -169,8 +176,9 @@ cwlb_status build_cache_hints(cwlb_ctx* ctx, const SpmmArgs& a, long long hot_ro
         taken += hist[b];
         theta = bucket_floor(b);
     }
-    // Nothing cold (every gathered column is hot): no hints.
-    ctx->hint_any_cold = theta != UINT_MAX && theta > 1;
+    // Nothing cold (every gathered column is hot): no hints.  With a
+    // sample, columns missing from it (count 0) are gathered and cold.
+    ctx->hint_any_cold = theta != UINT_MAX && (theta > 1 || sample > 1);
     if (ctx->hint_any_cold) {
         hipLaunchKernelGGL(cold_bits, dim3(static_cast<unsigned>((a.nnz + kBlock - 1) / kBlock)),
                            dim3(kBlock), 0, st, a.col_idx, static_cast<long long>(a.nnz),
