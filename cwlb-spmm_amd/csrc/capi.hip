@@ -292,8 +292,8 @@ cwlb_status cwlb_ctx_create(int device, void* stream, cwlb_ctx** out)
     hipError_t e = hipSuccess;
     for (auto& ev : c->ev)
         if (e == hipSuccess) e = hipEventCreate(&ev);
-    if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&c->d_status), sizeof(int));
-    if (e == hipSuccess) e = hipMemset(c->d_status, 0, sizeof(int));
+    if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&c->d_status), 2 * sizeof(int));
+    if (e == hipSuccess) e = hipMemset(c->d_status, 0, 2 * sizeof(int));
     if (e != hipSuccess) {
         cwlb_ctx_destroy(c);
         return hip_fail(e, "cwlb_ctx_create");
@@ -312,7 +312,7 @@ cwlb_status cwlb_ctx_destroy(cwlb_ctx* ctx)
     for (void* p : {static_cast<void*>(ctx->d_run_keys), static_cast<void*>(ctx->d_run_keys_sorted),
                     static_cast<void*>(ctx->d_run_order), ctx->d_sort_temp,
                     static_cast<void*>(ctx->d_col_counts), static_cast<void*>(ctx->d_count_hist),
-                    static_cast<void*>(ctx->d_hints)})
+                    static_cast<void*>(ctx->d_hints), static_cast<void*>(ctx->d_phase_bounds)})
         if (p) (void)hipFree(p);
     for (void* p : ctx->retired) (void)hipFree(p);
     for (int b = 0; b < 2; ++b) {
@@ -412,6 +412,39 @@ cwlb_status cwlb_ctx_get_occupancy(cwlb_ctx* ctx, int32_t* waves_per_simd)
     return CWLB_OK;
 }
 
+cwlb_status cwlb_ctx_set_column_phases(cwlb_ctx* ctx, int32_t phases)
+{
+    if (!ctx) return fail(CWLB_INVALID_ARG, "null context");
+    if (phases < 0 || phases > 64)
+        return fail(CWLB_INVALID_ARG, "phases must be in [0, 64] (0 or 1 = off)");
+    ctx->sched_phases = phases;
+    return CWLB_OK;
+}
+
+cwlb_status cwlb_ctx_get_column_phases(cwlb_ctx* ctx, int32_t* phases)
+{
+    if (!ctx || !phases) return fail(CWLB_INVALID_ARG, "null argument");
+    *phases = ctx->sched_phases;
+    return CWLB_OK;
+}
+
+cwlb_status cwlb_column_phase_bounds(cwlb_ctx* ctx, const int32_t* row_ptr,
+                                     const int32_t* col_idx, int32_t n_rows, int64_t nnz,
+                                     int64_t h_rows, int32_t phases, int32_t* out)
+{
+    if (!ctx) return fail(CWLB_INVALID_ARG, "null context");
+    if (phases < 2 || phases > 64)
+        return fail(CWLB_INVALID_ARG, "cwlb_column_phase_bounds: phases must be in [2, 64]");
+    if (n_rows < 0 || nnz < 0 || h_rows <= 0)
+        return fail(CWLB_INVALID_ARG,
+                    "cwlb_column_phase_bounds: n_rows >= 0, nnz >= 0 and h_rows > 0 required");
+    if (n_rows > 0 && (!row_ptr || !out || (nnz > 0 && !col_idx)))
+        return fail(CWLB_INVALID_ARG, "cwlb_column_phase_bounds: null array");
+    DeviceGuard g(ctx->device);
+    (void)hipGetLastError();
+    return launch_phase_bounds(ctx->stream, row_ptr, col_idx, n_rows, nnz, h_rows, phases, out);
+}
+
 cwlb_status cwlb_ctx_last_launch(cwlb_ctx* ctx, cwlb_launch_info* out)
 {
     if (!ctx || !out) return fail(CWLB_INVALID_ARG, "null argument");
@@ -456,9 +489,11 @@ cwlb_status cwlb_ctx_tune_schedule(cwlb_ctx* ctx, const int32_t* row_ptr, const 
     // placement are chosen without them.
     const long long keep_hot = ctx->sched_hot_bytes;
     const int keep_occ = ctx->sched_occupancy;
+    const int keep_phases = ctx->sched_phases;
     if (locality_out) {
         ctx->sched_hot_bytes = 0;
         ctx->sched_occupancy = 0;
+        ctx->sched_phases = 0;
     }
     float best_us = 0.0f;
     std::pair<int, int> best{0, 0};
@@ -492,6 +527,7 @@ cwlb_status cwlb_ctx_tune_schedule(cwlb_ctx* ctx, const int32_t* row_ptr, const 
         ctx->order_runs = -1;
         ctx->sched_hot_bytes = keep_hot;
         ctx->sched_occupancy = keep_occ;
+        ctx->sched_phases = keep_phases;
     };
     const int keep_order = ctx->sched_order, keep_xcd = ctx->sched_xcd;
     for (const auto& c : cands) {
@@ -601,6 +637,53 @@ cwlb_status cwlb_ctx_tune_schedule(cwlb_ctx* ctx, const int32_t* row_ptr, const 
                 ctx->sched_occupancy = 6;
                 ctx->sched_tasks_per_wave = m6;
             }
+        }
+        // Column phases, where they can pay: H beyond the Infinity Cache
+        // (>= 512 MB) and rows of 64 nonzeros or more on average (each
+        // phase reads and writes C once).  8, 12 and 16 phases, each with
+        // every slice count whose widest slice fits one vector per lane,
+        // at 16 and 64 tasks per wave, under the placement chosen above;
+        // kept when faster than the settings so far, re-timed first.
+        const long long h_bytes = h_rows * static_cast<long long>(K) * 4;
+        if (st == CWLB_OK && h_bytes >= (512ll << 20) && nnz >= 64ll * n_rows && K % 4 == 0) {
+            st = time_current(&base, nullptr);
+            const long long hot_kept = ctx->sched_hot_bytes;
+            const int occ_kept = ctx->sched_occupancy;
+            int best_p = 0, best_pm = best.first, best_psl = best.second;
+            for (int P : {8, 12, 16}) {
+                for (int sl : {1, 2, 4, 8}) {
+                    if (K / 4 < sl || (K / 4 + sl - 1) / sl > 64) continue;
+                    for (int m : {16, 64}) {
+                        if (st != CWLB_OK) break;
+                        ctx->sched_phases = P;
+                        ctx->sched_slices = sl;
+                        ctx->sched_tasks_per_wave = m;
+                        float med = 0.0f;
+                        st = time_current(&med, [](const cwlb_ctx* c) {
+                            return c->last_launch.column_phases > 1;
+                        });
+                        if (st == CWLB_OK && med > 0.0f && med < base) {
+                            base = med;
+                            best_p = P;
+                            best_pm = m;
+                            best_psl = sl;
+                        }
+                    }
+                }
+            }
+            ctx->sched_phases = best_p;
+            if (best_p) {
+                // The phased kernel takes neither hints nor the variant.
+                best.first = best_pm;
+                best.second = best_psl;
+                ctx->sched_hot_bytes = 0;
+                ctx->sched_occupancy = 0;
+            } else {
+                ctx->sched_hot_bytes = hot_kept;
+                ctx->sched_occupancy = occ_kept;
+            }
+            ctx->sched_tasks_per_wave = best.first;
+            ctx->sched_slices = best.second;
         }
         if (st != CWLB_OK) {
             restore(keep_order, keep_xcd);

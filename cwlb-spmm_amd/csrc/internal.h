@@ -20,9 +20,11 @@ struct cwlb_ctx {
     size_t total_mem = 0;
     char name[256] = {0};
     char arch[64] = {0};
-    // Device status word written by the kernels: bit 0 = a column index was
-    // outside [0, h_rows), bit 1 = an origin entry was outside [0, n_rows),
-    // bit 2 = a row's offsets left [0, nnz] or decreased.
+    // Device status words written by the kernels.  [0]: bit 0 = a column
+    // index was outside [0, h_rows), bit 1 = an origin entry was outside
+    // [0, n_rows), bit 2 = a row's offsets left [0, nnz] or decreased.
+    // [1]: the sequence number of the last column-phased call whose task
+    // list was not a chain.
     int* d_status = nullptr;
     // Schedule overrides (0 = automatic): tasks per wave, feature slices,
     // run order (1 = task order, 2 = by output row id) and block placement
@@ -54,6 +56,7 @@ struct cwlb_ctx {
     // one instead of rewriting or freeing it.
     bool order_captured = false;
     bool hints_captured = false;
+    bool phases_captured = false;
     std::vector<void*> retired;
     // Cache-policy hints of the feature-row gathers (0 = off): the hot set
     // in bytes of feature rows, the per-column in-degrees, their histogram
@@ -71,6 +74,19 @@ struct cwlb_ctx {
     unsigned hint_theta = 0;
     bool hint_any_cold = false;
     bool last_call_hinted = false;  // the last aggregation launch used hints
+    // Column phases (0 or 1 = none): the P - 1 interior row bounds, P - 1
+    // arrays of n_rows ints, with what they were built for, and the
+    // sequence number of the last phased call.
+    int sched_phases = 0;
+    int* d_phase_bounds = nullptr;
+    long long phase_cap = 0;
+    const void* phase_rp = nullptr;
+    const void* phase_col = nullptr;
+    long long phase_n_rows = -1;
+    long long phase_nnz = -1;
+    long long phase_h_rows = -1;
+    int phase_P = 0;
+    int phase_seq = 0;
     cwlb_launch_info last_launch{};  // the last aggregation launch's schedule
     // Pinned host staging of the host-pointer entry point: two buffers used
     // alternately, each with the event of the last transfer through it.
@@ -156,6 +172,17 @@ cwlb_status launch_fill_features(cwlb_ctx* ctx, float* H, int64_t rows, int32_t 
 // built but may_build is false (a stream under graph capture).
 cwlb_status build_cache_hints(cwlb_ctx* ctx, const SpmmArgs& a, long long hot_rows,
                               bool may_build, const unsigned long long** hints);
+
+// Builds (or reuses) the row bounds of `phases` column phases
+// (csrc/col_phases.hip) on ctx->stream.  *bounds is null when they would
+// have to be built but may_build is false (a stream under graph capture).
+cwlb_status build_column_phases(cwlb_ctx* ctx, const SpmmArgs& a, int phases, bool may_build,
+                                const int** bounds);
+
+// Enqueues the bounds kernel: out[(p - 1) * n_rows + r] for p in [1, phases).
+cwlb_status launch_phase_bounds(hipStream_t st, const int32_t* row_ptr, const int32_t* col_idx,
+                                int32_t n_rows, int64_t nnz, int64_t h_rows, int phases,
+                                int32_t* out);
 
 cwlb_status launch_reorder(cwlb_ctx* ctx, int32_t n_rows, int64_t nnz, const int32_t* row_ptr,
                            const int32_t* col_idx, const float* val, int32_t* origin,

@@ -198,6 +198,29 @@ __device__ __forceinline__ void vatomic_add(float* p, f4 v)
     unsafeAtomicAdd(p + 3, v.w);
 }
 
+// How a finished chunk reaches C: 0 stored, 1 added by a plain
+// read-modify-write (a row one segment owns, after the first column
+// phase), 2 added atomically (a row split between segments).
+template <bool PH, class Ch>
+__device__ __forceinline__ int write_mode(bool ph, bool first, const Ch& c)
+{
+    if constexpr (PH) {
+        if (ph) return c.own ? (first ? 0 : 1) : 2;
+    }
+    return (c.b == 0 && c.e == c.d) ? 0 : 2;
+}
+
+template <int VEC>
+__device__ __forceinline__ void write_row(float* p, typename VecT<VEC>::T v, int how)
+{
+    if (how == 0)
+        vstore_nt<VEC>(p, v);
+    else if (how == 1)
+        vstore_nt<VEC>(p, vload<VEC>(p) + v);
+    else
+        vatomic_add(p, v);
+}
+
 __device__ __forceinline__ int wave_max(int v)
 {
 #pragma unroll
@@ -214,6 +237,7 @@ struct Chunk {
     int b;     // chunk begin within the row
     int e;     // chunk end within the row
     int d;     // full degree (-1: malformed offsets)
+    int own;   // column phases only: the task covers the whole row
 };
 
 __device__ __forceinline__ Chunk row_chunk(const int* __restrict__ rp, int r, int rs, int re,
@@ -239,6 +263,37 @@ __device__ __forceinline__ Chunk row_chunk(const int* __restrict__ rp, int r, in
     c.b = b;
     c.e = e;
     return c;
+}
+
+// Row r's chunk under column phases.  With ph (the task list is a chain,
+// see zero_split_rows) the chunk is cut to the row's nonzeros of this
+// phase, [pb[r], pe[r]) -- the row's start for the first phase (pb null),
+// its end for the last (pe null) -- with the bounds clamped into the row,
+// so any non-decreasing bounds split the row exactly.  own records, before
+// the cut, whether the task covers the whole row: such a row belongs to
+// this one segment in every phase.
+template <bool PH>
+__device__ __forceinline__ Chunk task_chunk(const int* __restrict__ rp, int r, int rs, int re,
+                                            int fo, int ln, long long nnz, bool ph,
+                                            const int* __restrict__ pb,
+                                            const int* __restrict__ pe)
+{
+    if constexpr (!PH) {
+        return row_chunk(rp, r, rs, re, fo, ln, nnz);
+    } else {
+        int lo_abs = 0, hi_abs = 0;
+        if (ph && pb) lo_abs = pb[r];
+        if (ph && pe) hi_abs = pe[r];
+        Chunk c = row_chunk(rp, r, rs, re, fo, ln, nnz);
+        c.own = c.d > 0 && c.b == 0 && c.e == c.d;
+        if (ph && c.d > 0) {
+            const int lo = pb ? min(max(lo_abs - c.base, 0), c.d) : 0;
+            const int hi = pe ? min(max(hi_abs - c.base, lo), c.d) : c.d;
+            c.b = max(c.b, lo);
+            c.e = max(min(c.e, hi), c.b);
+        }
+        return c;
+    }
 }
 
 constexpr int cmin(int a, int b) { return a < b ? a : b; }
@@ -315,7 +370,11 @@ __device__ __forceinline__ void block_slice(int& slice, long long& jb, long long
                    : static_cast<long long>(bx >> 3) * P + q;
 }
 
-template <int VEC, int G, int R, int U, int SL, bool HN, bool O6>
+// PH: one launch of a column-phased call (pb, pe: this phase's row bounds,
+// first: the first phase, seq: the call's sequence number; status[1] ==
+// seq marks a task list that is not a chain, which then runs unphased in
+// the first launch and not at all in the others).
+template <int VEC, int G, int R, int U, int SL, bool HN, bool O6, bool PH>
 __global__ void __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(O6 ? 6 : 1)))
 spmm_mean_runs(const int* __restrict__ rp, const int* __restrict__ ci,
                const float* __restrict__ val, const int* __restrict__ origin, int n_rows,
@@ -323,7 +382,8 @@ spmm_mean_runs(const int* __restrict__ rp, const int* __restrict__ ci,
                const cwlb_task* __restrict__ tasks, long long n_tasks, int M, long long n_runs,
                long long n_blocks, long long chunk, const int* __restrict__ run_order,
                const unsigned long long* __restrict__ hints, float* __restrict__ C,
-               int* __restrict__ status)
+               int* __restrict__ status, const int* __restrict__ pb,
+               const int* __restrict__ pe, int first_phase, int seq)
 {
     static_assert(!HN || VEC == 4, "hinted gathers move 16 bytes per lane");
     using V = typename VecT<VEC>::T;
@@ -355,6 +415,15 @@ spmm_mean_runs(const int* __restrict__ rp, const int* __restrict__ ci,
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const long long pos = jb * kWaves + wv;
     if (pos >= n_runs) return;
+    // Column phases apply to chains only: rows whose whole range one
+    // segment covers are then stored in the first phase and added to,
+    // without atomics, in the others.
+    bool ph = false;
+    const bool first = !PH || first_phase != 0;
+    if constexpr (PH) {
+        ph = __builtin_amdgcn_readfirstlane(status[1]) != seq;
+        if (!ph && !first) return;
+    }
     int* __restrict__ wcol = s_col + wv * (kStage > 0 ? kStage : 1);
     float* __restrict__ wval = s_val + wv * (kStage > 0 ? kStage : 1);
     // run_order (optional) is a permutation of [0, n_runs): runs execute in
@@ -396,13 +465,14 @@ spmm_mean_runs(const int* __restrict__ rp, const int* __restrict__ ci,
                 Chunk my = {0, 0, 0, 0};
                 Chunk c0;
                 if constexpr (kEarly) {
-                    if (mine) my = row_chunk(rp, rr, rs, re, fo, ln, nnz);
+                    if (mine) my = task_chunk<PH>(rp, rr, rs, re, fo, ln, nnz, ph, pb, pe);
                     c0.base = __builtin_amdgcn_readfirstlane(my.base);
                     c0.b = __builtin_amdgcn_readfirstlane(my.b);
                     c0.e = __builtin_amdgcn_readfirstlane(my.e);
                     c0.d = __builtin_amdgcn_readfirstlane(my.d);
+                    if constexpr (PH) c0.own = __builtin_amdgcn_readfirstlane(my.own);
                 } else {
-                    c0 = row_chunk(rp, r, rs, re, fo, ln, nnz);
+                    c0 = task_chunk<PH>(rp, r, rs, re, fo, ln, nnz, ph, pb, pe);
                 }
                 const int len0 = c0.e - c0.b;
                 if (len0 >= kLong) {
@@ -479,17 +549,11 @@ spmm_mean_runs(const int* __restrict__ rp, const int* __restrict__ ci,
                     } else if (slot == 0) {
                         float* crow = Cs + static_cast<size_t>(o) * ld;
                         const float fd = static_cast<float>(c0.d);
-                        const bool full = (c0.b == 0 && c0.e == c0.d);
+                        const int how = write_mode<PH>(ph, first, c0);
 #pragma unroll
                         for (int q = 0; q < R; ++q) {
                             const int f = fl + G * q;
-                            if (f < F) {
-                                const V res = vdiv(acc[q], fd);
-                                if (full)
-                                    vstore_nt<VEC>(crow + f * VEC, res);
-                                else
-                                    vatomic_add(crow + f * VEC, res);
-                            }
+                            if (f < F) write_row<VEC>(crow + f * VEC, vdiv(acc[q], fd), how);
                         }
                     }
                     ++r;
@@ -499,7 +563,7 @@ spmm_mean_runs(const int* __restrict__ rp, const int* __restrict__ ci,
                 // ---------------- short rows: one row per slot, RU rows per slot
                 const int lane = lane_g;
                 if constexpr (!kEarly) {
-                    if (mine) my = row_chunk(rp, rr, rs, re, fo, ln, nnz);
+                    if (mine) my = task_chunk<PH>(rp, rr, rs, re, fo, ln, nnz, ph, pb, pe);
                 }
                 const int mylen = my.e - my.b;
                 // The group: the leading rows that are short, start where the
@@ -626,11 +690,13 @@ spmm_mean_runs(const int* __restrict__ rp, const int* __restrict__ ci,
                 for (int u = 0; u < RU; ++u) {
                     const int gi = u * NS + fresh(slot);
                     const int o = __shfl(myo, gi);
-                    const int d = __shfl(my.d, gi);
-                    const int b = __shfl(my.b, gi);
-                    const int e = __shfl(my.e, gi);
+                    Chunk cu;
+                    cu.d = __shfl(my.d, gi);
+                    cu.b = __shfl(my.b, gi);
+                    cu.e = __shfl(my.e, gi);
+                    if constexpr (PH) cu.own = __shfl(my.own, gi);
                     if (gi < cnt) {
-                        if (d < 0) {
+                        if (cu.d < 0) {
                             bad |= 4;
                             continue;
                         }
@@ -639,25 +705,23 @@ spmm_mean_runs(const int* __restrict__ rp, const int* __restrict__ ci,
                             continue;
                         }
                         float* crow = Cs + static_cast<size_t>(o) * ld;
-                        if (d == 0) {
+                        if (cu.d == 0) {
+                            if (first) {
 #pragma unroll
-                            for (int q = 0; q < R; ++q) {
-                                const int f = fl + G * q;
-                                if (f < F) vstore_nt<VEC>(crow + f * VEC, vzero<VEC>());
-                            }
-                        } else if (e > b) {
-                            const float fd = static_cast<float>(d);
-                            const bool full = (b == 0 && e == d);
-#pragma unroll
-                            for (int q = 0; q < R; ++q) {
-                                const int f = fl + G * q;
-                                if (f < F) {
-                                    const V res = vdiv(acc[u][q], fd);
-                                    if (full)
-                                        vstore_nt<VEC>(crow + f * VEC, res);
-                                    else
-                                        vatomic_add(crow + f * VEC, res);
+                                for (int q = 0; q < R; ++q) {
+                                    const int f = fl + G * q;
+                                    if (f < F) vstore_nt<VEC>(crow + f * VEC, vzero<VEC>());
                                 }
+                            }
+                        } else if (cu.e > cu.b || (PH && ph && first && cu.own)) {
+                            // (an owned row with no nonzero in the first phase
+                            // is stored as zeros all the same)
+                            const float fd = static_cast<float>(cu.d);
+                            const int how = write_mode<PH>(ph, first, cu);
+#pragma unroll
+                            for (int q = 0; q < R; ++q) {
+                                const int f = fl + G * q;
+                                if (f < F) write_row<VEC>(crow + f * VEC, vdiv(acc[u][q], fd), how);
                             }
                         }
                     }
@@ -672,6 +736,26 @@ spmm_mean_runs(const int* __restrict__ rp, const int* __restrict__ ci,
     // reading its first and last task.
     const long long t0 = run * M;
     const int cnt = static_cast<int>(min(static_cast<long long>(M), n_tasks - t0));
+    if constexpr (PH) {
+        if (ph) {
+            // A chain under column phases: the run takes, whole, every row
+            // whose first nonzero lies in its tasks -- from its first task's
+            // row (the next row when that task continues a row begun
+            // earlier) to its last task's row, completed -- so each row has
+            // one wave and no atomics.  The chain's ends keep their offsets:
+            // the first task's start, and the last task's end in its row.
+            const cwlb_task a = tasks[t0];
+            const cwlb_task z = tasks[t0 + cnt - 1];
+            const cwlb_task zl = tasks[n_tasks - 1];
+            const bool head = t0 == 0;
+            const int rs = (head || a.first_row_offset == 0) ? a.row_start : a.row_start + 1;
+            const int fo = head ? a.first_row_offset : 0;
+            const int ln = z.row_end == zl.row_end ? zl.last_row_nnz : 0;
+            if (rs < z.row_end) run_segment(rs, z.row_end, fo, ln);
+            if (bad) atomicOr(status, bad);
+            return;
+        }
+    }
     for (int w = 0; w < cnt; w += 64) {
         const int wn = min(64, cnt - w);
         const long long tw = t0 + w;
@@ -712,12 +796,17 @@ spmm_mean_runs(const int* __restrict__ rp, const int* __restrict__ ci,
 // row it cannot follow further is cleared, which costs only a store when
 // the row is later stored whole.  So only the tasks that open a row read
 // row offsets.  The wave clears the marked rows with coalesced stores.
-// Block 0 also resets the status word.
+// Block 0 also resets the status word.  For a column-phased call (seq > 0)
+// the pass also checks that the list is a chain -- every task well formed
+// and continuing its predecessor, so that no two tasks share a nonzero and
+// a row covered whole by one segment is touched by no other -- and
+// otherwise writes seq into status[1] (which nothing resets: a stale value
+// differs from every later call's seq).
 template <int VEC>
 __global__ void __launch_bounds__(kBlock)
 zero_split_rows(const int* __restrict__ rp, const int* __restrict__ origin, int n_rows,
                 long long nnz, const cwlb_task* __restrict__ tasks, long long n_tasks, int M,
-                int K, float* __restrict__ C, int* __restrict__ status)
+                int K, float* __restrict__ C, int* __restrict__ status, int seq)
 {
     const int lane = threadIdx.x & 63;
     const long long t = static_cast<long long>(blockIdx.x) * kBlock + threadIdx.x;
@@ -729,8 +818,11 @@ zero_split_rows(const int* __restrict__ rp, const int* __restrict__ origin, int 
     bool brk = true;    // task t starts a segment (lanes past the end count as starts)
     bool ends = false;  // task t's chunk of its first row reaches that row's end
     int o = -1;         // original id of the row task t leaves open
+    bool unlinked = false;  // task t breaks the chain
     if (t < n_tasks) {
         brk = segment_break(prev, cur, t % M, n_rows);
+        unlinked = !task_well_formed(cur, n_rows) ||
+                   (t > 0 && (!task_well_formed(prev, n_rows) || !continues(prev, cur)));
         const int rs = cur.row_start, re = cur.row_end;
         const int fo = cur.first_row_offset, ln = cur.last_row_nnz;
         int r = -1;  // the candidate row
@@ -746,6 +838,7 @@ zero_split_rows(const int* __restrict__ rp, const int* __restrict__ origin, int 
         }
         if (o >= n_rows) o = -1;
     }
+    if (seq > 0 && __ballot(unlinked) != 0ull && lane == 0) status[1] = seq;
     const unsigned long long mb = __ballot(brk);
     const unsigned long long me = __ballot(ends);
     if (o >= 0 && lane < 63) {
@@ -826,29 +919,53 @@ struct Plan {
     bool o6;               // the 6-waves-per-SIMD variant
     const int* order;      // that order (device), set at launch
     const unsigned long long* hints;  // cold-column bits (device) or null
+    int phases;            // column phases (1 = none)
+    // The launch's phase: its row bounds (null = the row's own start / end),
+    // whether it is the first, and the call's sequence number.
+    const int* pb;
+    const int* pe;
+    int first;
+    int seq;
 };
 
 // Launches one instantiation; returns its resident waves per CU at most
 // (from its register and LDS use, queried once per instantiation).
-template <int VEC, int G, int R, int SL, bool HN = false, bool O6 = false>
+template <int VEC, int G, int R, int SL, bool HN = false, bool O6 = false, bool PH = false>
 int launch_main(hipStream_t st, const SpmmArgs& a, const Plan& p, int* status)
 {
     constexpr int U = (R == 1) ? 8 : (R == 2) ? 4 : (R <= 4) ? 2 : 1;
     static const int waves_per_cu = [] {
         int blocks = 0;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                &blocks, reinterpret_cast<const void*>(&spmm_mean_runs<VEC, G, R, U, SL, HN, O6>),
+                &blocks,
+                reinterpret_cast<const void*>(&spmm_mean_runs<VEC, G, R, U, SL, HN, O6, PH>),
                 kBlock, 0) != hipSuccess)
             blocks = 0;
         return blocks * kWaves;
     }();
-    hipLaunchKernelGGL((spmm_mean_runs<VEC, G, R, U, SL, HN, O6>),
+    hipLaunchKernelGGL((spmm_mean_runs<VEC, G, R, U, SL, HN, O6, PH>),
                        dim3(static_cast<unsigned>(p.grid)), dim3(kBlock), 0, st, a.row_ptr,
                        a.col_idx, a.val, a.origin, a.n_rows, static_cast<long long>(a.nnz), a.H,
                        static_cast<long long>(a.h_rows), a.K, a.tasks,
                        static_cast<long long>(a.n_tasks), p.M, p.runs, p.blocks, p.chunk, p.order,
-                       p.hints, a.C, status);
+                       p.hints, a.C, status, p.pb, p.pe, p.first, p.seq);
     return waves_per_cu;
+}
+
+// Column phases: 16-byte lanes, one vector per lane, no hints, the
+// standard kernel.
+template <int SL>
+int dispatch_phased(hipStream_t st, const SpmmArgs& a, const Plan& p, int* status, int G)
+{
+    switch (G) {
+    case 1: return launch_main<4, 1, 1, SL, false, false, true>(st, a, p, status);
+    case 2: return launch_main<4, 2, 1, SL, false, false, true>(st, a, p, status);
+    case 4: return launch_main<4, 4, 1, SL, false, false, true>(st, a, p, status);
+    case 8: return launch_main<4, 8, 1, SL, false, false, true>(st, a, p, status);
+    case 16: return launch_main<4, 16, 1, SL, false, false, true>(st, a, p, status);
+    case 32: return launch_main<4, 32, 1, SL, false, false, true>(st, a, p, status);
+    default: return launch_main<4, 64, 1, SL, false, false, true>(st, a, p, status);
+    }
 }
 
 // Feature slices of one lane group (one vector per lane) under cache hints.
@@ -885,6 +1002,7 @@ int dispatch_width(hipStream_t st, const SpmmArgs& a, const Plan& p, int* status
         int G = 1;
         while (G < F) G <<= 1;
         if constexpr (VEC == 4) {
+            if (p.phases > 1) return dispatch_phased<SL>(st, a, p, status, G);
             if (p.o6 && G >= 4 && G <= 16) {
                 if (p.hints) return dispatch_o6<SL, true>(st, a, p, status, G);
                 return dispatch_o6<SL, false>(st, a, p, status, G);
@@ -933,7 +1051,8 @@ void launch_zero(hipStream_t st, const SpmmArgs& a, const Plan& p, int* status)
     const long long blocks = (a.n_tasks + kBlock - 1) / kBlock;
     hipLaunchKernelGGL(zero_split_rows<VEC>, dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0,
                        st, a.row_ptr, a.origin, a.n_rows, static_cast<long long>(a.nnz), a.tasks,
-                       static_cast<long long>(a.n_tasks), p.M, a.K, a.C, status);
+                       static_cast<long long>(a.n_tasks), p.M, a.K, a.C, status,
+                       p.phases > 1 ? p.seq : 0);
 }
 
 int pick_vec(const SpmmArgs& a)
@@ -1005,6 +1124,17 @@ Plan make_plan(const cwlb_ctx* ctx, const SpmmArgs& a, bool per_task)
     p.o6 = !per_task && ctx->sched_occupancy == 6 && p.vec == 4 && f4 > 2 && f4 <= 16;
     p.order = nullptr;
     p.hints = nullptr;
+    // Column phases: 16-byte lanes and at most 64 vectors per slice; they
+    // replace the occupancy variant and the cache hints.
+    p.phases = 1;
+    if (!per_task && ctx->sched_phases > 1 && p.vec == 4 && f4 <= 64 && a.h_rows > 0) {
+        p.phases = ctx->sched_phases;
+        p.o6 = false;
+    }
+    p.pb = nullptr;
+    p.pe = nullptr;
+    p.first = 1;
+    p.seq = 0;
     return p;
 }
 
@@ -1029,9 +1159,22 @@ cwlb_status launch_spmm_mean(cwlb_ctx* ctx, const SpmmArgs& a, bool zero_all, bo
     hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
     CWLB_HIP_TRY(hipStreamIsCapturing(st, &capture));
     const bool may_build = capture == hipStreamCaptureStatusNone;
+    const bool work = a.n_tasks > 0 && a.K > 0;
+    // Column phases: the row bounds of the phases (built, or reused under
+    // capture; without them the call runs unphased, with the same result).
+    const int* bounds = nullptr;
+    if (p.phases > 1 && work) {
+        const cwlb_status s = build_column_phases(ctx, a, p.phases, may_build, &bounds);
+        if (s != CWLB_OK) return s;
+    }
+    if (!bounds) p.phases = 1;
+    if (p.phases > 1) {
+        ctx->phase_seq = ctx->phase_seq >= 0x7fffffff ? 1 : ctx->phase_seq + 1;
+        p.seq = ctx->phase_seq;
+    }
     // Cache hints: 16-byte lanes, one vector per lane and slice, and the
     // feature matrix addressable by 32-bit byte offsets.
-    if (!per_task && ctx->sched_hot_bytes > 0 && p.vec == 4 && a.n_tasks > 0 && a.K > 0 &&
+    if (!per_task && p.phases == 1 && ctx->sched_hot_bytes > 0 && p.vec == 4 && a.n_tasks > 0 && a.K > 0 &&
         (a.K / 4 + p.sl - 1) / p.sl <= 64 &&
         static_cast<unsigned long long>(a.h_rows) * a.K * 4ull <= 0xFFFFFFFFull) {
         const long long hot_rows = ctx->sched_hot_bytes / (4ll * a.K);
@@ -1061,7 +1204,9 @@ cwlb_status launch_spmm_mean(cwlb_ctx* ctx, const SpmmArgs& a, bool zero_all, bo
     ctx->last_launch.waves_per_simd = p.o6 ? 6 : 0;
     ctx->last_launch.grid_blocks = a.n_tasks > 0 && a.K > 0 ? p.grid : 0;
     ctx->last_launch.max_waves_per_cu = 0;
-    if (!zero_all && a.n_tasks > 0 && a.K > 0) {
+    ctx->last_launch.column_phases = p.phases;
+    // A phased call always runs the clearing pass: it also checks the chain.
+    if ((!zero_all || p.phases > 1) && work) {
         if (p.vec == 4) launch_zero<4>(st, a, p, ctx->d_status);
         else if (p.vec == 2) launch_zero<2>(st, a, p, ctx->d_status);
         else launch_zero<1>(st, a, p, ctx->d_status);
@@ -1070,13 +1215,21 @@ cwlb_status launch_spmm_mean(cwlb_ctx* ctx, const SpmmArgs& a, bool zero_all, bo
     }
     CWLB_HIP_TRY(hipGetLastError());
     if (record_events) CWLB_HIP_TRY(hipEventRecord(ctx->ev[1], st));
-    if (a.n_tasks > 0 && a.K > 0) {
+    if (work) {
         int waves = 0;
-        if (p.vec == 4) waves = dispatch_main<4>(st, a, p, ctx->d_status);
-        else if (p.vec == 2) waves = dispatch_main<2>(st, a, p, ctx->d_status);
-        else waves = dispatch_main<1>(st, a, p, ctx->d_status);
+        for (int ph = 0; ph < p.phases; ++ph) {
+            // Phase ph reads the bounds ph - 1 and ph of the P - 1 stored
+            // per row (the row's own start and end at the outer phases).
+            const long long n = a.n_rows;
+            p.pb = ph > 0 ? bounds + (ph - 1) * n : nullptr;
+            p.pe = ph < p.phases - 1 ? bounds + ph * n : nullptr;
+            p.first = ph == 0;
+            if (p.vec == 4) waves = dispatch_main<4>(st, a, p, ctx->d_status);
+            else if (p.vec == 2) waves = dispatch_main<2>(st, a, p, ctx->d_status);
+            else waves = dispatch_main<1>(st, a, p, ctx->d_status);
+            CWLB_HIP_TRY(hipGetLastError());
+        }
         ctx->last_launch.max_waves_per_cu = waves;
-        CWLB_HIP_TRY(hipGetLastError());
     }
     if (record_events) CWLB_HIP_TRY(hipEventRecord(ctx->ev[2], st));
     return CWLB_OK;

@@ -25,6 +25,7 @@ EXPORTS = [
     "cwlb_ctx_set_stream", "cwlb_ctx_synchronize", "cwlb_ctx_device_info", "cwlb_ctx_set_schedule",
     "cwlb_ctx_set_locality", "cwlb_ctx_set_cache_hints", "cwlb_ctx_get_cache_hints",
     "cwlb_ctx_last_launch", "cwlb_ctx_set_occupancy", "cwlb_ctx_get_occupancy",
+    "cwlb_ctx_set_column_phases", "cwlb_ctx_get_column_phases", "cwlb_column_phase_bounds",
     "cwlb_ctx_tune_schedule",
     "cwlb_spmm_mean_f32", "cwlb_spmm_mean_f32_large_k", "cwlb_spmm_mean_f32_host",
     "cwlb_spmm_mean_f32_noalloc",
@@ -81,7 +82,7 @@ class LaunchInfo(C.Structure):
                 ("run_order", C.c_int32), ("xcd_blocks", C.c_int32),
                 ("cache_hints", C.c_int32), ("vector_width", C.c_int32),
                 ("waves_per_simd", C.c_int32), ("max_waves_per_cu", C.c_int32),
-                ("grid_blocks", C.c_int64)]
+                ("column_phases", C.c_int32), ("grid_blocks", C.c_int64)]
 
 
 class DeviceInfo(C.Structure):
@@ -123,6 +124,9 @@ def lib():
         L.cwlb_ctx_last_launch.argtypes = [vp, C.POINTER(LaunchInfo)]
         L.cwlb_ctx_set_occupancy.argtypes = [vp, i32]
         L.cwlb_ctx_get_occupancy.argtypes = [vp, C.POINTER(i32)]
+        L.cwlb_ctx_set_column_phases.argtypes = [vp, i32]
+        L.cwlb_ctx_get_column_phases.argtypes = [vp, C.POINTER(i32)]
+        L.cwlb_column_phase_bounds.argtypes = [vp, vp, vp, i32, i64, i64, i32, vp]
         L.cwlb_ctx_tune_schedule.argtypes = [vp, vp, vp, vp, vp, i32, i64, vp, i64, i32, vp, i64,
                                              vp, i32, C.POINTER(i32), C.POINTER(i32), vp]
         spmm = [vp, vp, vp, vp, vp, i32, i64, vp, i64, i32, vp, i64, vp, u32, C.POINTER(Timing)]
@@ -326,6 +330,19 @@ class Context:
         v = i32()
         check(lib().cwlb_ctx_get_occupancy(self.h, C.byref(v)))
         return v.value
+
+    def set_column_phases(self, phases=0):
+        check(lib().cwlb_ctx_set_column_phases(self.h, int(phases)))
+
+    def column_phases(self):
+        v = i32()
+        check(lib().cwlb_ctx_get_column_phases(self.h, C.byref(v)))
+        return v.value
+
+    def column_phase_bounds(self, row_ptr, col_idx, n_rows, nnz, h_rows, phases, out):
+        """cwlb_column_phase_bounds on device tensors (enqueued on the stream)."""
+        check(lib().cwlb_column_phase_bounds(self.h, _ptr(row_ptr), _ptr(col_idx), int(n_rows),
+                                             int(nnz), int(h_rows), int(phases), _ptr(out)))
 
     def tune_schedule(self, row_ptr, col_idx, val, origin, n_rows, nnz, H, h_rows, K, tasks,
                       n_tasks, C_out, trials=3, locality=False):

@@ -156,6 +156,47 @@ cwlb_status cwlb_ctx_get_cache_hints(cwlb_ctx* ctx, int64_t* hot_bytes);
 cwlb_status cwlb_ctx_set_occupancy(cwlb_ctx* ctx, int32_t waves_per_simd);
 cwlb_status cwlb_ctx_get_occupancy(cwlb_ctx* ctx, int32_t* waves_per_simd);
 
+/* Column phases of later SpMM calls on this context.  phases = 0 or 1 (the
+ * default): one pass.  phases = P in [2, 64]: the task list is executed P
+ * times, pass p gathering only the nonzeros whose column lies in
+ * [p * h_rows / P, (p + 1) * h_rows / P), so that the feature rows all
+ * waves read at a time span 1/P of H and stay in the caches.  A row that
+ * one stretch of consecutive tasks covers whole (see CWLB_SPMM_PER_TASK) is
+ * stored in the first pass and added to in the others without atomics,
+ * which reads and writes C P times: it pays when H is well beyond the
+ * 256 MB Infinity Cache, the columns of a row are spread over H and rows
+ * hold many more nonzeros than 2P (measured: a 240k-row block model with
+ * 480 nonzeros per row and K = 600, 16 phases, 15% faster).  The per-row
+ * bounds of the passes (P - 1 ints per row, see cwlb_column_phase_bounds)
+ * are built by the first call after a change of the row or column array,
+ * n_rows, nnz, h_rows or P into a context-owned buffer (no
+ * synchronisation) and reused later; under graph capture they are only
+ * reused (otherwise the call runs in one pass).  Any bounds give the same
+ * result, so bounds left over from earlier array contents only cost speed.
+ * Applies to task lists that are chains -- every task well formed and
+ * starting where its predecessor ended, as cwlb_partition's lists are --
+ * which the device checks on every call; any other list runs in one pass.
+ * Applies with 16-byte aligned H and C, K a multiple of 4 and at most 256
+ * floats per feature slice, without CWLB_SPMM_PER_TASK; replaces the
+ * occupancy variant and the cache hints while on.  Results agree with the
+ * one-pass ones within the float tolerance (each phase's partial sum is
+ * divided and added separately).  No counterpart in the reference;
+ * cwlb_ctx_tune_schedule tries it. */
+cwlb_status cwlb_ctx_set_column_phases(cwlb_ctx* ctx, int32_t phases);
+cwlb_status cwlb_ctx_get_column_phases(cwlb_ctx* ctx, int32_t* phases);
+
+/* The interior bounds of P column phases (2 <= P <= 64), enqueued on the
+ * context's stream from device arrays: out[(p - 1) * n_rows + r] =
+ * row_ptr[r] + the number of nonzeros of row r whose column c has
+ * floor(c * P / h_rows) < p, for p in [1, P) (a column below 0 counts in
+ * band 0, one at or above h_rows in band P - 1; a row whose offsets leave
+ * [0, nnz] or decrease gets 0).  out holds (P - 1) * n_rows ints.  No
+ * counterpart in the reference; the column-phased aggregation builds these
+ * itself, tests read them here. */
+cwlb_status cwlb_column_phase_bounds(cwlb_ctx* ctx, const int32_t* row_ptr,
+                                     const int32_t* col_idx, int32_t n_rows, int64_t nnz,
+                                     int64_t h_rows, int32_t phases, int32_t* out);
+
 /* The schedule the last aggregation launch on this context used, as the
  * automatic choices and the context's settings resolved it (all zero before
  * the first launch).  No counterpart in the reference; tests and the bench
@@ -170,7 +211,11 @@ typedef struct cwlb_launch_info {
     int32_t waves_per_simd;  /* 6 for the occupancy variant, else 0 */
     int32_t max_waves_per_cu; /* resident waves per CU the kernel's register
                                  and LDS use allow */
-    int64_t grid_blocks;     /* work-groups of the aggregation kernel */
+    int32_t column_phases;   /* column phases planned (1 = none; a task list
+                                that is not a chain runs unphased all the
+                                same, see cwlb_ctx_set_column_phases) */
+    int64_t grid_blocks;     /* work-groups of the aggregation kernel (per
+                                phase) */
 } cwlb_launch_info;
 cwlb_status cwlb_ctx_last_launch(cwlb_ctx* ctx, cwlb_launch_info* out);
 
@@ -260,10 +305,17 @@ cwlb_status cwlb_spmm_mean_f32_large_k(cwlb_ctx* ctx, const int32_t* row_ptr,
  * tasks per wave returned can be 1); then with cache hints of 24, 48 and
  * 96 MB (cwlb_ctx_set_cache_hints), the fastest kept on the context (0 =
  * none; read it with cwlb_ctx_get_cache_hints); then the standard kernel
- * again with those hints when the variant was kept.  In that mode every timing before the hint
- * sizes runs without hints, and every timing before the occupancy variant
- * with the standard kernel, whatever the context held.  C receives the
- * result.  Synchronises.  No counterpart in the reference, whose one task
+ * again with those hints when the variant was kept; then, when H holds at
+ * least 512 MB, K is a multiple of 4 and rows average 64 nonzeros or more,
+ * with 8, 12 and 16 column phases (cwlb_ctx_set_column_phases) at every
+ * slice count they take and 16 or 64 tasks per wave: the fastest is kept
+ * when it beats the settings so far (its tasks per wave and slices are
+ * then the ones returned; read the phases with
+ * cwlb_ctx_get_column_phases), otherwise phases stay off.  In that mode
+ * every timing before the hint sizes runs without hints, every timing
+ * before the occupancy variant with the standard kernel, and every timing
+ * before the phases in one pass, whatever the context held.  C receives
+ * the result.  Synchronises.  No counterpart in the reference, whose one task
  * per work-group has nothing to tune; like its S search, it is meant to run
  * once per graph before timed runs. */
 cwlb_status cwlb_ctx_tune_schedule(cwlb_ctx* ctx, const int32_t* row_ptr, const int32_t* col_idx,

@@ -1,0 +1,363 @@
+"""GPU parity of the column-phased aggregation (cwlb_ctx_set_column_phases).
+
+The phased path runs a chain of tasks P times, phase p gathering the
+nonzeros whose column lies in band p of the feature matrix, each row owned
+by one wave (stored in the first phase, added to in the others).  Its
+results must be the reference's (the oracle, src/parallelMatrix.cpp:
+148-236) within the parity tolerance |gpu - ref| <= 1e-6 + 1e-5 |ref|, for
+every run length, slice count and phase count, for chains that start and
+end inside rows, and lists that are not chains must run in one pass with
+the one-pass results.  The device-built bounds must equal their host
+restatement exactly.
+"""
+import numpy as np
+import pytest
+
+import oracle
+from conftest import SKEWED_COSTS, UNIT_COSTS
+from cwlb_amd import capi, synth, workloads
+from test_column_phases import phase_bounds
+from test_gpu_spmm import check, custom_graph, dev, oracle_pair, problem, run_gpu, torch_mod
+
+pytestmark = pytest.mark.gpu
+
+
+def set_phased(ctx, P, M, SL, order=1, xcd=1):
+    ctx.set_schedule(M, SL)
+    ctx.set_locality(order, xcd)
+    ctx.set_column_phases(P)
+
+
+@pytest.fixture
+def reset(gpu_ctx):
+    yield
+    gpu_ctx.set_column_phases(0)
+    gpu_ctx.set_schedule(0, 0)
+    gpu_ctx.set_locality(0, 0)
+
+
+def expected_phases(K, SL, P):
+    """Phases the launch runs: 16-byte lanes and at most 64 vectors per slice."""
+    if P < 2 or K % 4 or K < 4:
+        return 1
+    sl = SL if (SL > 0 and K // 4 >= SL) else 1
+    return P if -(-(K // 4) // sl) <= 64 else 1
+
+
+def device_bounds(ctx, rp, ci, h_rows, P):
+    torch = torch_mod()
+    n = len(rp) - 1
+    out = torch.full(((P - 1) * max(n, 1),), -7, dtype=torch.int32, device="cuda")
+    ctx.column_phase_bounds(dev(rp), dev(ci), n, len(ci), h_rows, P, out)
+    torch.cuda.synchronize()
+    return out.cpu().numpy()[:(P - 1) * n].reshape(P - 1, n)
+
+
+@pytest.mark.parametrize("P", [2, 3, 16, 64])
+def test_bounds_match_host(gpu_ctx, P):
+    """Sorted and unsorted rows, columns below 0 and at or past h_rows, a
+    row of 3000 nonzeros (many 64-wide steps), empty rows and rows whose
+    offsets leave [0, nnz] or decrease: the device bounds equal the host
+    restatement exactly."""
+    rng = np.random.default_rng(P)
+    n, h = 2000, 777
+    deg = rng.integers(0, 90, n)
+    deg[5] = 3000
+    deg[rng.integers(0, n, 200)] = 0
+    rp = np.concatenate([[0], np.cumsum(deg)]).astype(np.int32)
+    ci = rng.integers(-3, h + 4, rp[-1]).astype(np.int32)
+    for r in range(0, n, 2):
+        ci[rp[r]:rp[r + 1]].sort()
+    got = device_bounds(gpu_ctx, rp, ci, h, P)
+    assert np.array_equal(got, phase_bounds(rp, ci, h, P))
+    bad = rp.copy()
+    bad[100] = bad[101] + 5       # row 100 decreases
+    bad[-1] = rp[-1] + 50         # the last row passes nnz
+    got = device_bounds(gpu_ctx, bad, ci, h, P)
+    assert np.array_equal(got, phase_bounds(bad, ci, h, P))
+    assert (got[:, 100] == 0).all() and (got[:, n - 1] == 0).all()
+
+
+def test_bounds_arguments(gpu_ctx):
+    torch = torch_mod()
+    rp, ci = dev(np.array([0, 1], np.int32)), dev(np.array([0], np.int32))
+    out = torch.zeros(64, dtype=torch.int32, device="cuda")
+    for P, h in ((1, 1), (65, 1), (2, 0)):
+        with pytest.raises(capi.CwlbError) as e:
+            gpu_ctx.column_phase_bounds(rp, ci, 1, 1, h, P, out)
+        assert e.value.status == capi.INVALID_ARG
+    gpu_ctx.column_phase_bounds(rp, ci, 0, 0, 1, 2, out)  # nothing to do
+
+
+# (P, tasks per wave, slices)
+PHASED = [(2, 1, 1), (4, 3, 2), (16, 16, 4), (8, 64, 8), (64, 5, 1), (3, 200, 2), (12, 16, 0)]
+PHASED_IDS = [f"p{p}m{m}s{s}" for p, m, s in PHASED]
+
+
+@pytest.mark.parametrize("P,M,SL", PHASED, ids=PHASED_IDS)
+@pytest.mark.parametrize("cfg", [1, 2, 3, 4, 5])
+def test_small_configs(gpu_ctx, reset, cfg, P, M, SL):
+    """Each configuration family at reduced size (K = 64, or 600 for the
+    block model, where slices of at most 64 vectors need 4 or 8 of them)."""
+    g = workloads.small(cfg)
+    K = 600 if cfg == 3 else 64
+    S = workloads.candidate_s(g.nnz, 256)[1]
+    p = problem(g, SKEWED_COSTS, S)
+    H = synth.features(g.n, K, workloads.FEATURE_SEED)
+    set_phased(gpu_ctx, P, M, SL)
+    print(f"cfg={cfg} P={P} M={M} SL={SL} n={g.n} tasks={len(p.tasks)}", flush=True)
+    got, _ = run_gpu(gpu_ctx, p, H)
+    assert gpu_ctx.last_launch()["column_phases"] == expected_phases(K, SL, P)
+    ref32, ref64 = oracle_pair(p, g, H)
+    check(got, ref32)
+    check(got, ref64)
+
+
+@pytest.mark.parametrize("K", [4, 8, 12, 64, 100, 128, 256, 260, 512])
+def test_feature_widths(gpu_ctx, reset, K):
+    """Phases apply with at most 64 vectors per slice; other widths run in
+    one pass; every width gives the reference's result."""
+    g = workloads.small(4, seed=3)
+    p = problem(g, UNIT_COSTS, 5)
+    H = synth.features(g.n, K, 2)
+    for SL in (1, 4):
+        set_phased(gpu_ctx, 6, 8, SL)
+        got, _ = run_gpu(gpu_ctx, p, H)
+        assert gpu_ctx.last_launch()["column_phases"] == expected_phases(K, SL, 6), (K, SL)
+        check(got, oracle.spmm_mean_f32(p.row_ptr, p.col_idx, p.val, p.origin, H, p.tasks))
+
+
+@pytest.mark.parametrize("M", [1, 4, 64])
+def test_chains_inside_rows(gpu_ctx, reset, M):
+    """Sub-lists of a partition start and end inside split rows.  With C
+    holding earlier values, rows outside keep them, the first row (partial,
+    not cleared) is added onto them, the last is cleared and added: the
+    phased result equals the one-pass result; with ZERO_OUTPUT it equals
+    the oracle."""
+    torch = torch_mod()
+    rng = np.random.default_rng(M)
+    g = workloads.small(4, seed=5)
+    K = 32
+    p = problem(g, UNIT_COSTS, 3)
+    H = synth.features(g.n, K, 1)
+    split = np.nonzero(p.tasks[:, 2] > 0)[0]
+    d_rp, d_ci, d_v, d_o = dev(p.row_ptr), dev(p.col_idx), dev(p.val), dev(p.origin)
+    d_H = dev(H)
+    prior = torch.from_numpy(synth.features(g.n, K, 9)).cuda()
+    for _ in range(4):
+        k, j = np.sort(rng.choice(split, 2, replace=False))
+        sub = p.tasks[k:j + 1]
+        d_t = dev(np.ascontiguousarray(sub).reshape(-1))
+        outs = []
+        for P in (0, 5):
+            set_phased(gpu_ctx, P, M, 2)
+            C = prior.clone()
+            gpu_ctx.spmm(d_rp, d_ci, d_v, d_o, g.n, g.nnz, d_H, g.n, K, d_t, len(sub), C)
+            outs.append(C.cpu().numpy())
+            assert gpu_ctx.last_launch()["column_phases"] == max(P, 1)
+        np.testing.assert_allclose(outs[1], outs[0], rtol=1e-5, atol=1e-6)
+        C = torch.full((g.n, K), float("nan"), dtype=torch.float32, device="cuda")
+        gpu_ctx.spmm(d_rp, d_ci, d_v, d_o, g.n, g.nnz, d_H, g.n, K, d_t, len(sub), C,
+                     flags=capi.ZERO_OUTPUT)
+        check(C.cpu().numpy(), oracle.spmm_mean_f32(p.row_ptr, p.col_idx, p.val, p.origin, H,
+                                                    sub))
+
+
+@pytest.mark.parametrize("how", ["shuffled", "gaps", "malformed_task"])
+def test_lists_that_are_not_chains(gpu_ctx, reset, how):
+    """Lists that break the chain run in one pass inside the phased launch
+    sequence: the reference's result (with ZERO_OUTPUT for gapped lists),
+    then a chain on the same context runs phased again."""
+    rng = np.random.default_rng(len(how))
+    g = workloads.small(4, seed=8)
+    K = 64
+    p = problem(g, SKEWED_COSTS, 4)
+    H = synth.features(g.n, K, 3)
+    t = p.tasks.copy()
+    if how == "shuffled":
+        t = t[rng.permutation(len(t))]
+    elif how == "gaps":
+        t = t[rng.random(len(t)) > 0.1]
+    else:
+        t = np.concatenate([t[:50], [[3, 3, 0, 0]], t[50:]]).astype(np.int32)
+    q = workloads.Prepared(p.n, p.nnz, p.origin, p.row_ptr, p.col_idx, p.val, t, 0, 0.0)
+    set_phased(gpu_ctx, 7, 16, 2)
+    got, _ = run_gpu(gpu_ctx, q, H, flags=capi.ZERO_OUTPUT)
+    check(got, oracle.spmm_mean_f32(p.row_ptr, p.col_idx, p.val, p.origin, H, t))
+    got, _ = run_gpu(gpu_ctx, p, H)
+    check(got, oracle.spmm_mean_f32(p.row_ptr, p.col_idx, p.val, p.origin, H, p.tasks))
+
+
+def test_hub_row_degree_zero_rows_and_zero_output(gpu_ctx, reset, rng):
+    """A row of 5,000 nonzeros split into many tasks among empty rows and
+    rows whose nonzeros all lie in one band; with and without ZERO_OUTPUT."""
+    n = 6000
+    deg = np.zeros(n, np.int64)
+    deg[17] = 5000
+    deg[rng.integers(0, n, 400)] = rng.integers(1, 9, 400)
+    rp = np.concatenate([[0], np.cumsum(deg)]).astype(np.int32)
+    ci = rng.integers(0, n, rp[-1]).astype(np.int32)
+    ci[rp[100]:rp[101]] = n - 1  # (row 100 may be empty) the last band only
+    val = rng.uniform(-2, 2, rp[-1]).astype(np.float32)
+    g = custom_graph(rp, ci, val)
+    H = synth.features(n, 64, 1)
+    for S in (1, 3, 64, 5000):
+        p = problem(g, UNIT_COSTS, S)
+        ref32, ref64 = oracle_pair(p, g, H)
+        for P, M, flags in ((4, 1, 0), (16, 64, capi.ZERO_OUTPUT), (64, 7, 0)):
+            set_phased(gpu_ctx, P, M, 1)
+            got, _ = run_gpu(gpu_ctx, p, H, flags=flags)
+            check(got, ref32)
+            check(got, ref64)
+
+
+def test_rewritten_columns_keep_results_right(gpu_ctx, reset):
+    """Bounds built for earlier contents of col_idx (same pointer, sizes and
+    P, so they are reused) only move nonzeros between phases."""
+    torch = torch_mod()
+    g = workloads.small(2, seed=4)
+    K = 64
+    p = problem(g, SKEWED_COSTS, 5)
+    H = synth.features(g.n, K, 5)
+    d_rp, d_ci, d_v, d_o = dev(p.row_ptr), dev(p.col_idx), dev(p.val), dev(p.origin)
+    d_t = dev(np.ascontiguousarray(p.tasks).reshape(-1))
+    d_H = dev(H)
+    C = torch.zeros((g.n, K), dtype=torch.float32, device="cuda")
+    set_phased(gpu_ctx, 8, 16, 1)
+    gpu_ctx.spmm(d_rp, d_ci, d_v, d_o, g.n, g.nnz, d_H, g.n, K, d_t, len(p.tasks), C)
+    other = np.random.default_rng(2).integers(0, g.n, g.nnz).astype(np.int32)
+    d_ci.copy_(torch.from_numpy(other))
+    gpu_ctx.spmm(d_rp, d_ci, d_v, d_o, g.n, g.nnz, d_H, g.n, K, d_t, len(p.tasks), C)
+    check(C.cpu().numpy(), oracle.spmm_mean_f32(p.row_ptr, other, p.val, p.origin, H, p.tasks))
+
+
+@pytest.mark.parametrize("bad", ["decreasing", "beyond_nnz", "column"])
+def test_bad_entries_are_reported(gpu_ctx, reset, bad):
+    """Bad row offsets and column indices are reported as with one pass; a
+    good call afterwards clears the report."""
+    g = workloads.small(1, seed=2)
+    H = synth.features(g.n, 32, 3)
+    p = problem(g, UNIT_COSTS, 6)
+    good_rp, good_ci = p.row_ptr, p.col_idx
+    if bad == "column":
+        ci = p.col_idx.copy()
+        ci[len(ci) // 3] = g.n + 5
+        p.col_idx = ci
+    else:
+        rp = p.row_ptr.copy()
+        r = len(rp) // 2
+        if bad == "decreasing":
+            rp[r] = rp[r + 1] + 3
+        else:
+            rp[-1] = p.nnz + 100
+        p.row_ptr = rp
+    set_phased(gpu_ctx, 5, 8, 1)
+    with pytest.raises(capi.CwlbError) as e:
+        run_gpu(gpu_ctx, p, H)
+    assert e.value.status == capi.INVALID_ARG
+    p.row_ptr, p.col_idx = good_rp, good_ci
+    got, _ = run_gpu(gpu_ctx, p, H)
+    check(got, oracle.spmm_mean_f32(p.row_ptr, p.col_idx, p.val, p.origin, H, p.tasks))
+
+
+@pytest.mark.parametrize("built", [True, False], ids=["bounds_built", "bounds_unbuilt"])
+def test_graph_capture_and_replay(gpu_ctx, reset, built):
+    """A phased call captured into a HIP graph after an eager call built its
+    bounds replays the phases; without built bounds the captured call runs
+    in one pass.  Every replay, between eager work, gives the eager
+    result."""
+    torch = torch_mod()
+    g = workloads.small(4, seed=21)
+    K = 64
+    p = problem(g, SKEWED_COSTS, 9)
+    d_rp, d_ci, d_v, d_o = dev(p.row_ptr), dev(p.col_idx), dev(p.val), dev(p.origin)
+    d_t = dev(np.ascontiguousarray(p.tasks, np.int32).reshape(-1))
+    H = dev(synth.features(g.n, K, 4))
+    C = torch.zeros((g.n, K), dtype=torch.float32, device="cuda")
+    set_phased(gpu_ctx, 6 if built else 5, 8, 2)
+    if built:
+        gpu_ctx.spmm(d_rp, d_ci, d_v, d_o, g.n, g.nnz, H, g.n, K, d_t, len(p.tasks), C)
+    else:
+        # bounds for another phase count: not reusable under capture
+        gpu_ctx.set_column_phases(9)
+        gpu_ctx.spmm(d_rp, d_ci, d_v, d_o, g.n, g.nnz, H, g.n, K, d_t, len(p.tasks), C)
+        gpu_ctx.set_column_phases(5)
+    eager = C.clone()
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        gpu_ctx.set_stream(side.cuda_stream)
+        with torch.cuda.graph(graph, stream=side):
+            gpu_ctx.spmm(d_rp, d_ci, d_v, d_o, g.n, g.nnz, H, g.n, K, d_t, len(p.tasks), C,
+                         timed=False)
+    gpu_ctx.set_stream(torch.cuda.current_stream().cuda_stream)
+    assert gpu_ctx.last_launch()["column_phases"] == (6 if built else 1)
+    torch.cuda.synchronize()
+    for i in range(4):
+        C.fill_(float(i))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        np.testing.assert_allclose(C.cpu().numpy(), eager.cpu().numpy(), rtol=1e-5, atol=1e-6)
+        # eager phased calls on another list between replays
+        gpu_ctx.spmm(d_rp, d_ci, d_v, d_o, g.n, g.nnz, H, g.n, K, d_t, len(p.tasks) // 2,
+                     torch.zeros_like(C))
+    ref32 = oracle.spmm_mean_f32(p.row_ptr, p.col_idx, p.val, p.origin, H.cpu().numpy(), p.tasks)
+    np.testing.assert_allclose(C.cpu().numpy(), ref32, rtol=1e-5, atol=1e-6)
+
+
+def test_phase_arguments(gpu_ctx, reset):
+    for bad in (-1, 65):
+        with pytest.raises(capi.CwlbError) as e:
+            gpu_ctx.set_column_phases(bad)
+        assert e.value.status == capi.INVALID_ARG
+    gpu_ctx.set_column_phases(64)
+    assert gpu_ctx.column_phases() == 64
+    gpu_ctx.set_column_phases(0)
+    assert gpu_ctx.column_phases() == 0
+
+
+def test_per_task_flag_runs_one_pass(gpu_ctx, reset):
+    g = workloads.small(2, seed=3)
+    p = problem(g, SKEWED_COSTS, 5)
+    H = synth.features(g.n, 32, 1)
+    set_phased(gpu_ctx, 8, 8, 1)
+    got, _ = run_gpu(gpu_ctx, p, H, flags=capi.PER_TASK)
+    assert gpu_ctx.last_launch()["column_phases"] == 1
+    check(got, oracle.spmm_mean_f32(p.row_ptr, p.col_idx, p.val, p.origin, H, p.tasks))
+
+
+def test_tuner_tries_phases(gpu_ctx, reset):
+    """A graph where phases may pay (H of 512 MB, 64 nonzeros per row): the
+    tuner's choice, phases or not, leaves a context whose calls give the
+    reference's result on sampled rows (the full oracle is too slow here)."""
+    torch = torch_mod()
+    n, deg, K = 131072, 64, 1024
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    rp = torch.arange(0, (n + 1) * deg, deg, dtype=torch.int32, device="cuda")
+    ci = torch.randint(0, n, (n * deg,), generator=gen, dtype=torch.int32, device="cuda")
+    ci = ci.view(n, deg).sort(dim=1).values.reshape(-1).contiguous()
+    val = torch.ones(n * deg, dtype=torch.float32, device="cuda")
+    origin = torch.arange(n, dtype=torch.int32, device="cuda")
+    tasks_np = capi.partition(rp.cpu().numpy(), SKEWED_COSTS,
+                              capi.capacity_from_s(40, SKEWED_COSTS))
+    tasks = dev(np.ascontiguousarray(tasks_np).reshape(-1))
+    H = torch.empty((n, K), dtype=torch.float32, device="cuda")
+    gpu_ctx.fill_features(H, n, K, 3)
+    C = torch.full((n, K), float("nan"), dtype=torch.float32, device="cuda")
+    m, sl, loc = gpu_ctx.tune_schedule(rp, ci, val, origin, n, n * deg, H, n, K, tasks,
+                                       len(tasks_np), C, trials=1, locality=True)
+    P = gpu_ctx.column_phases()
+    print(f"tuned m={m} sl={sl} loc={loc} phases={P}", flush=True)
+    assert P in (0, 8, 12, 16)
+    C.fill_(float("nan"))
+    gpu_ctx.spmm(rp, ci, val, origin, n, n * deg, H, n, K, tasks, len(tasks_np), C)
+    assert gpu_ctx.last_launch()["column_phases"] == max(P, 1)
+    rows = np.random.default_rng(1).choice(n, 64, replace=False)
+    ci_h = ci.view(n, deg)[torch.from_numpy(rows).cuda().long()].long()
+    want = H[ci_h].double().mean(dim=1).cpu().numpy()
+    got = C[torch.from_numpy(rows).cuda().long()].double().cpu().numpy()
+    np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-6)
+    del H, C
+    torch.cuda.empty_cache()
