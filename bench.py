@@ -91,7 +91,7 @@ def schedule_args(S, sched):
     return ["--s", str(S), "--tasks-per-wave", str(sched["tasks_per_wave"]),
             "--slices", str(sched["feature_slices"]), "--run-order", str(sched["run_order"]),
             "--xcd-blocks", str(sched["xcd_blocks"]), "--hot-mb", str(sched["hot_bytes"] >> 20),
-            "--occupancy", str(sched["occupancy"])]
+            "--occupancy", str(sched["occupancy"]), "--phases", str(sched.get("phases", 0))]
 
 
 def read_counter_csv(path):
@@ -107,12 +107,26 @@ def read_counter_csv(path):
     return vals
 
 
-def measure_counters(args, cfg, K, S, sched):
+# Counters that add up over the dispatches of one call (a column-phased call
+# dispatches the aggregation kernel once per phase).
+ADDITIVE = {"FETCH_SIZE", "WRITE_SIZE", "TCC_HIT_sum", "TCC_MISS_sum"}
+
+
+def per_call_value(counter, values, per_call):
+    """One call's value of a counter read on every dispatch: the mean over
+    the dispatches, times the dispatches of one call when it adds up."""
+    mean = sum(values) / len(values)
+    return mean * per_call if counter in ADDITIVE else mean
+
+
+def measure_counters(args, cfg, K, S, sched, per_call=1):
     """Replays the timed launch (same workload, S and schedule) in child
     processes under rocprofv3, one counter pass each, each with a 1 GiB
-    device-to-device copy as the known-size reference.  Returns the mean
-    counter values of the aggregation kernel's dispatches, the copy's, and
-    the kernel's name; raises RuntimeError when a pass fails."""
+    device-to-device copy as the known-size reference.  Returns the
+    aggregation kernel's counter values per call (the mean over its
+    dispatches, times the per_call dispatches of one call for the additive
+    counters), the copy's, and the kernel's name; raises RuntimeError when a
+    pass fails."""
     rocprof = shutil.which("rocprofv3") or "/opt/rocm/bin/rocprofv3"
     if not os.path.exists(rocprof):
         raise RuntimeError("rocprofv3 not found")
@@ -138,8 +152,9 @@ def measure_counters(args, cfg, K, S, sched):
         shutil.rmtree(tmp, ignore_errors=True)
         for (kname, cname), v in vals.items():
             if "spmm_mean_runs" in kname:
-                out["kernel"][cname] = sum(v) / len(v)
+                out["kernel"][cname] = per_call_value(cname, v, per_call)
                 out["dispatches"] = len(v)
+                out["dispatches_per_call"] = per_call
                 out["name"] = kname
             elif "copyBuffer" in kname:
                 out["copy"][cname] = v[-1]  # the probe is the last copy of the run
@@ -177,6 +192,7 @@ def pmc_child(args):
     ctx.set_locality(args.run_order, args.xcd_blocks)
     ctx.set_cache_hints(args.hot_mb << 20)
     ctx.set_occupancy(args.occupancy)
+    ctx.set_column_phases(args.phases)
     for _ in range(1 + args.steps):
         ctx.spmm(d[0], d[1], d[2], d[3], g.n, g.nnz, H, g.n, K, d[4], len(tasks), C,
                  large_k=large_k)
@@ -224,6 +240,7 @@ def roofline_record(counters, err, b_alg, b_min, main_us, launched):
                      "WRITE_SIZE_kib": round(k["WRITE_SIZE"], 1),
                      "fetch_scale": round(fetch_scale, 5), "write_scale": round(write_scale, 5),
                      "copy_probe_bytes": probe, "dispatches": counters["dispatches"],
+                     "dispatches_per_call": counters.get("dispatches_per_call", 1),
                      "how": "rocprofv3 --pmc, one pass per counter group, on a replay of the "
                             "timed launch in a child process; scales from a 1 GiB "
                             "device-to-device copy in the same runs"}})
@@ -242,6 +259,7 @@ def segment_size_sweep(ctx, call, tune, dev, tasks_for, cfg, costs, S, trials):
     ctx.set_locality(0, 0)
     ctx.set_cache_hints(0)
     ctx.set_occupancy(0)
+    ctx.set_column_phases(0)
     for _ in range(3):
         call(d_t, len(tk), False)
     auto_us = float(np.mean([call(d_t, len(tk), True).main_us for _ in range(trials)]))
@@ -253,7 +271,7 @@ def segment_size_sweep(ctx, call, tune, dev, tasks_for, cfg, costs, S, trials):
             "tuned_us": round(tuned_us, 1),
             "schedule": {"tasks_per_wave": m, "feature_slices": sl, "run_order": order,
                          "xcd_blocks": xcd, "hot_bytes": ctx.cache_hints(),
-                         "occupancy": ctx.occupancy()},
+                         "occupancy": ctx.occupancy(), "phases": ctx.column_phases()},
             "tasks_match_reference_fixture": reference_partition_match(cfg, S, costs, tk)}
 
 
@@ -303,10 +321,14 @@ def preprocessing_times(ctx, g, rp, costs, S, tasks, reorder_host_ms):
 def schedule_build_times(call_fresh, sched):
     """Wall time (ms) that the chosen schedule's one-off builds add to the
     first call on a new context: the cache hints (column in-degrees, their
-    histogram, one bit per nonzero) and the run order sorted by output row.
-    Each is the first call's time minus the second's, on a context that has
-    only that setting."""
-    out = {"cache_hint_build_ms": None, "run_order_build_ms": None}
+    histogram, one bit per nonzero), the run order sorted by output row and
+    the column phases' row bounds.  Each is the first call's time minus the
+    second's, on a context that has only that setting."""
+    out = {"cache_hint_build_ms": None, "run_order_build_ms": None,
+           "column_phase_build_ms": None}
+    if sched.get("phases", 0) > 1:
+        first, second = call_fresh({"phases": sched["phases"]})
+        out["column_phase_build_ms"] = round(first - second, 2)
     if sched["hot_bytes"] > 0:
         first, second = call_fresh({"hot_bytes": sched["hot_bytes"]})
         out["cache_hint_build_ms"] = round(first - second, 2)
@@ -338,6 +360,8 @@ def parse_args():
     ap.add_argument("--slices", type=int, default=0)
     ap.add_argument("--occupancy", type=int, default=0, choices=(0, 6),
                     help="fixed schedule: 6 = the 6-waves-per-SIMD kernel variant")
+    ap.add_argument("--phases", type=int, default=0,
+                    help="fixed schedule: column phases (cwlb_ctx_set_column_phases)")
     ap.add_argument("--run-order", type=int, default=0,
                     help="fixed run order (cwlb_ctx_set_locality: 1 task order, 2 by output row)")
     ap.add_argument("--xcd-blocks", type=int, default=0,
@@ -418,7 +442,7 @@ def main():
     # is kept.  A fixed schedule (--tasks-per-wave etc.) or --no-tune ranks
     # the S by the automatic schedule instead.
     fixed = bool(args.tasks_per_wave or args.slices or args.run_order or args.xcd_blocks
-                 or args.hot_mb or args.occupancy)
+                 or args.hot_mb or args.occupancy or args.phases)
     tuning = not fixed and not args.no_tune
     cands = [args.s] if args.s else workloads.candidate_s(g.nnz, info.compute_units)
     best = None
@@ -431,6 +455,7 @@ def main():
         ctx.set_locality(0, 0)
         ctx.set_cache_hints(0)
         ctx.set_occupancy(0)
+        ctx.set_column_phases(0)
         for _ in range(5):
             call(d_t, len(tk), False)
         us = float(np.mean([call(d_t, len(tk), True).total_us for _ in range(10)]))
@@ -442,7 +467,7 @@ def main():
             t_tune += time.perf_counter() - t0
             rec["schedule"] = {"tasks_per_wave": m, "feature_slices": sl, "run_order": order,
                                "xcd_blocks": xcd, "hot_bytes": ctx.cache_hints(),
-                               "occupancy": ctx.occupancy()}
+                               "occupancy": ctx.occupancy(), "phases": ctx.column_phases()}
             for _ in range(3):
                 call(d_t, len(tk), False)
             rank = float(np.mean([call(d_t, len(tk), True).total_us for _ in range(10)]))
@@ -458,12 +483,13 @@ def main():
     log(f"preprocessing: {prep}")
     # Launch schedule for this graph and S (0, 0 = the automatic choice).
     schedule = {"tasks_per_wave": 0, "feature_slices": 0, "run_order": 0, "xcd_blocks": 0,
-                "hot_bytes": 0, "occupancy": 0, "tuned": False,
+                "hot_bytes": 0, "occupancy": 0, "phases": 0, "tuned": False,
                 "automatic_schedule_us": round(float(auto_us), 1)}
     if fixed:
         schedule.update(tasks_per_wave=args.tasks_per_wave, feature_slices=args.slices,
                         run_order=args.run_order, xcd_blocks=args.xcd_blocks,
-                        hot_bytes=args.hot_mb << 20, occupancy=args.occupancy)
+                        hot_bytes=args.hot_mb << 20, occupancy=args.occupancy,
+                        phases=args.phases)
         log(f"fixed schedule: {schedule}")
     elif tuning:
         schedule.update(tuned, tuned=True, tuning_ms=round(t_tune * 1e3, 1))
@@ -474,6 +500,7 @@ def main():
         c.set_locality(sched["run_order"], sched["xcd_blocks"])
         c.set_cache_hints(sched["hot_bytes"])
         c.set_occupancy(sched["occupancy"])
+        c.set_column_phases(sched["phases"])
 
     apply(ctx, schedule)
 
@@ -503,7 +530,7 @@ def main():
         c = capi.Context(0, stream.cuda_stream)
         try:
             only = dict(schedule)
-            only.update(hot_bytes=0, run_order=0)
+            only.update(hot_bytes=0, run_order=0, phases=0)
             only.update(setting)
             apply(c, only)
             walls = []
@@ -519,7 +546,8 @@ def main():
 
     prep.update(schedule_build_times(call_fresh, schedule))
     log(f"schedule builds: hints {prep['cache_hint_build_ms']} ms, "
-        f"run order {prep['run_order_build_ms']} ms")
+        f"run order {prep['run_order_build_ms']} ms, "
+        f"phase bounds {prep['column_phase_build_ms']} ms")
     # The reference's structure (one task per wave, one atomic add per
     # partial segment), for comparison.
     pt = [ctx.spmm(d_rp, d_ci, d_v, d_o, g.n, g.nnz, H, g.n, K, d_t, T, C,
@@ -568,7 +596,8 @@ def main():
         del d_rp, d_ci, d_v, d_o, H, C, d_t
         torch.cuda.empty_cache()
         try:
-            counters = measure_counters(args, cfg, K, S, schedule)
+            counters = measure_counters(args, cfg, K, S, schedule,
+                                        per_call=launched.get("column_phases", 1))
             pmc_err = None
         except (RuntimeError, OSError, KeyError, ZeroDivisionError) as e:
             pmc_err = str(e)

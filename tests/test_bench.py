@@ -81,7 +81,18 @@ def test_schedule_args_fix_the_launch(bench):
              "hot_bytes": 48 << 20, "occupancy": 0}
     args = bench.schedule_args(63, sched)
     assert args == ["--s", "63", "--tasks-per-wave", "64", "--slices", "2", "--run-order", "0",
-                    "--xcd-blocks", "0", "--hot-mb", "48", "--occupancy", "0"]
+                    "--xcd-blocks", "0", "--hot-mb", "48", "--occupancy", "0", "--phases", "0"]
+    sched["phases"] = 16
+    assert bench.schedule_args(63, sched)[-2:] == ["--phases", "16"]
+
+
+def test_counters_per_call(bench):
+    """A call of P column phases dispatches the kernel P times: traffic and
+    L2 accesses add up over them, the occupancy is a mean."""
+    assert bench.per_call_value("FETCH_SIZE", [10.0, 30.0], 16) == pytest.approx(320.0)
+    assert bench.per_call_value("TCC_MISS_sum", [4.0], 3) == pytest.approx(12.0)
+    assert bench.per_call_value("MeanOccupancyPerCU", [10.0, 30.0], 16) == pytest.approx(20.0)
+    assert bench.per_call_value("WRITE_SIZE", [5.0, 7.0], 1) == pytest.approx(6.0)
 
 
 def test_more_than_one_gpu_is_refused():
