@@ -952,7 +952,8 @@ FULL_LAUNCHES = {
         (1, 64, 0, 1, 1, 48 * MB, 6, 0)],
     5: [(2, 1, 1, 2, 2, 0, 6, 0), (2, 2, 1, 2, 2, 0, 6, 0), (1, 4, 1, 2, 2, 0, 6, 0),
         (2, None), (2, 0, 0, 0, 0, 0, 0, 0), (2, 0, 0, 0, 0, 0, 0, capi.PER_TASK)],
-    3: [(0, 64, 1, 2, 2, 0, 0, 0), (0, None), (0, 0, 0, 0, 0, 0, 0, 0), (2, 8, 1, 2, 2, 0, 0, 0)],
+    3: [(0, 64, 1, 2, 2, 0, 0, 0), (0, None), (0, 0, 0, 0, 0, 0, 0, 0), (2, 8, 1, 2, 2, 0, 0, 0),
+        (1, 64, 8, 2, 2, 0, 0, 0, 12), (1, 16, 4, 1, 1, 0, 0, 0, 16)],
     2: [(1, 8, 1, 1, 1, 0, 6, 0), (1, None), (2, 0, 0, 0, 0, 0, 0, capi.PER_TASK)],
 }
 
@@ -1002,11 +1003,12 @@ def test_full_size_launches_vs_oracle(gpu_ctx, cfg):
                 m, sl, loc = gpu_ctx.tune_schedule(*args, trials=3, locality=True)
                 flags = 0
             else:
-                _, m, sl, order, xcd, hot, occ, flags = launch
+                _, m, sl, order, xcd, hot, occ, flags = launch[:8]
                 gpu_ctx.set_schedule(m, sl)
                 gpu_ctx.set_locality(order, xcd)
                 gpu_ctx.set_cache_hints(hot)
                 gpu_ctx.set_occupancy(occ)
+                gpu_ctx.set_column_phases(launch[8] if len(launch) > 8 else 0)
             C.fill_(float("nan"))
             gpu_ctx.spmm(*args, flags=flags)
             info = gpu_ctx.last_launch()
@@ -1016,16 +1018,19 @@ def test_full_size_launches_vs_oracle(gpu_ctx, cfg):
                 assert info["tasks_per_wave"] == m or m == 0, what
                 assert info["feature_slices"] == sl or sl == 0, what
                 assert info["cache_hints"] == int(hot > 0), what
+                assert info["column_phases"] == max(launch[8] if len(launch) > 8 else 1, 1), what
             _assert_close_on_device(torch, C, ref_dev, what)
             gpu_ctx.set_schedule(0, 0)
             gpu_ctx.set_locality(0, 0)
             gpu_ctx.set_cache_hints(0)
             gpu_ctx.set_occupancy(0)
+            gpu_ctx.set_column_phases(0)
     finally:
         gpu_ctx.set_schedule(0, 0)
         gpu_ctx.set_locality(0, 0)
         gpu_ctx.set_cache_hints(0)
         gpu_ctx.set_occupancy(0)
+        gpu_ctx.set_column_phases(0)
 
 
 def test_async_call_reports_bad_column_at_synchronize(gpu_ctx):
@@ -1229,6 +1234,7 @@ def test_tune_schedule(gpu_ctx):
         gpu_ctx.set_locality(0, 0)
         gpu_ctx.set_cache_hints(0)
         gpu_ctx.set_occupancy(0)
+        gpu_ctx.set_column_phases(0)
 
 
 def test_run_order_reused_across_task_lists(gpu_ctx):
