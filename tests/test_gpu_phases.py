@@ -127,6 +127,21 @@ def test_feature_widths(gpu_ctx, reset, K):
         check(got, oracle.spmm_mean_f32(p.row_ptr, p.col_idx, p.val, p.origin, H, p.tasks))
 
 
+@pytest.mark.parametrize("K", [1028, 2048, 2052])
+def test_large_k_entry(gpu_ctx, reset, K):
+    """The large-K entry takes phases when its slices are narrow enough (8
+    slices of at most 64 float4 up to K = 2,048), else runs in one pass."""
+    g = workloads.small(2, seed=7)
+    p = problem(g, SKEWED_COSTS, 6)
+    H = synth.features(g.n, K, 4)
+    ref = oracle.spmm_mean_f32(p.row_ptr, p.col_idx, p.val, p.origin, H, p.tasks)
+    for SL in (8, 4):
+        set_phased(gpu_ctx, 5, 16, SL)
+        got, _ = run_gpu(gpu_ctx, p, H, large_k=True)
+        assert gpu_ctx.last_launch()["column_phases"] == expected_phases(K, SL, 5), (K, SL)
+        check(got, ref)
+
+
 @pytest.mark.parametrize("M", [1, 4, 64])
 def test_chains_inside_rows(gpu_ctx, reset, M):
     """Sub-lists of a partition start and end inside split rows.  With C
