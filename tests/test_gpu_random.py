@@ -1,6 +1,7 @@
 """Seeded random cross-product of graph family, K, S, costs and launch
 schedule (run length, feature slices, run order, XCD placement, cache hints,
-occupancy variant, flags, feature-view alignment) against the oracle.
+occupancy variant, column phases, flags, feature-view alignment) against the
+oracle.
 
 The structured tests in test_gpu_spmm.py cover each setting on fixed graphs;
 these cases draw combinations that no structured test names, with the same
@@ -19,7 +20,7 @@ from cwlb_amd import capi, synth, workloads
 pytestmark = pytest.mark.gpu
 
 RTOL, ATOL = 1e-5, 1e-6
-N_CASES = 192
+N_CASES = 256
 K_CHOICES = [1, 2, 3, 4, 7, 8, 12, 16, 31, 32, 48, 60, 64, 96, 100, 128, 200, 256, 300, 384,
              512, 600, 1024, 1028, 1100]
 
@@ -43,6 +44,9 @@ def draw_case(i):
         "flags": [0, 0, 0, capi.ZERO_OUTPUT, capi.PER_TASK][int(r.integers(5))],
         "h_offset": [0, 0, 0, 1, 2][int(r.integers(5))],  # floats past the allocation start
         "occupancy": [0, 0, 6][int(r.integers(3))],
+        # drawn from its own stream, so the other settings of a case do not
+        # depend on it
+        "phases": [0, 0, 2, 5, 16][int(np.random.default_rng(5000 + i).integers(5))],
     }
 
 
@@ -72,6 +76,7 @@ def test_random_schedule_case(gpu_ctx, i):
     gpu_ctx.set_locality(c["order"], c["xcd"])
     gpu_ctx.set_cache_hints(c["hot_rows"] * 4 * K)
     gpu_ctx.set_occupancy(c["occupancy"])
+    gpu_ctx.set_column_phases(c["phases"])
     try:
         gpu_ctx.spmm(d_rp, d_ci, d_v, d_o, g.n, g.nnz, d_H, g.n, K, d_t, len(p.tasks), C,
                      flags=c["flags"], large_k=large_k)
@@ -81,6 +86,7 @@ def test_random_schedule_case(gpu_ctx, i):
         gpu_ctx.set_locality(0, 0)
         gpu_ctx.set_cache_hints(0)
         gpu_ctx.set_occupancy(0)
+        gpu_ctx.set_column_phases(0)
 
     ref = oracle.spmm_mean_f32(p.row_ptr, p.col_idx, p.val, p.origin, H, p.tasks)
     np.testing.assert_allclose(C.cpu().numpy(), ref, rtol=RTOL, atol=ATOL, err_msg=str(c))
@@ -106,5 +112,12 @@ def test_random_schedule_case(gpu_ctx, i):
         2 if K % 2 == 0 and c["h_offset"] % 2 == 0 else 1)
     assert info["vector_width"] == expect_vec, info
     f4 = -(-(K // 4) // info["feature_slices"])  # vectors of the widest slice
-    o6 = (c["occupancy"] == 6 and not per_task and expect_vec == 4 and 2 < f4 <= 16)
+    # Column phases: 16-byte lanes, at most 64 vectors per slice; they
+    # replace the occupancy variant and the cache hints.
+    phased = c["phases"] > 1 and not per_task and expect_vec == 4 and f4 <= 64
+    assert info["column_phases"] == (c["phases"] if phased else 1), (info, c)
+    o6 = (c["occupancy"] == 6 and not per_task and expect_vec == 4 and 2 < f4 <= 16
+          and not phased)
     assert info["waves_per_simd"] == (6 if o6 else 0), (info, c)
+    if phased:
+        assert info["cache_hints"] == 0, (info, c)
