@@ -547,25 +547,35 @@ cwlb_status cwlb_ctx_tune_schedule(cwlb_ctx* ctx, const int32_t* row_ptr, const 
     ctx->sched_tasks_per_wave = best.first;
     ctx->sched_slices = best.second;
     if (locality_out) {
-        // Locality placements for the best schedule: runs sorted by output
-        // row (the order is computed once and reused), with interleaved or
-        // contiguous XCD stretches.
+        // Locality placements for the best schedule: the context's own, and
+        // runs sorted by output row with interleaved or contiguous XCD
+        // stretches.  The three are timed afresh, in two interleaved rounds
+        // (the best of each kept): two placements within a few percent of
+        // each other (the mesh's) are otherwise decided by clock drift, and
+        // the first stage's minimum over many candidates is biased low.
         int best_order = keep_order, best_xcd = keep_xcd;
-        for (const auto& loc : {std::pair<int, int>{2, 1}, {2, 2}}) {
-            ctx->sched_order = loc.first;
-            ctx->sched_xcd = loc.second;
-            ctx->order_runs = -1;
-            float med = 0.0f;
-            st = time_current(&med, nullptr);
+        {
+            const std::pair<int, int> locs[3] = {{keep_order, keep_xcd}, {2, 1}, {2, 2}};
+            float loc_us[3] = {0.0f, 0.0f, 0.0f};
+            for (int round = 0; round < 2 && st == CWLB_OK; ++round) {
+                for (int i = 0; i < 3 && st == CWLB_OK; ++i) {
+                    ctx->sched_order = locs[i].first;
+                    ctx->sched_xcd = locs[i].second;
+                    float med = 0.0f;
+                    st = time_current(&med, nullptr);
+                    if (st == CWLB_OK && (loc_us[i] == 0.0f || med < loc_us[i])) loc_us[i] = med;
+                }
+            }
             if (st != CWLB_OK) {
                 restore(keep_order, keep_xcd);
                 return st;
             }
-            if (med < best_us) {
-                best_us = med;
-                best_order = loc.first;
-                best_xcd = loc.second;
-            }
+            int k = 0;
+            for (int i = 1; i < 3; ++i)
+                if (loc_us[i] < loc_us[k]) k = i;
+            best_order = locs[k].first;
+            best_xcd = locs[k].second;
+            best_us = loc_us[k];
         }
         ctx->sched_order = best_order;
         ctx->sched_xcd = best_xcd;

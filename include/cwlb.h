@@ -297,9 +297,10 @@ cwlb_status cwlb_spmm_mean_f32_large_k(cwlb_ctx* ctx, const int32_t* row_ptr,
  * the fastest on the context (cwlb_ctx_set_schedule); the choice is also
  * returned through the optional out pointers (0, 0 = the automatic schedule
  * won).  With locality_out non-null (two int32), the fastest schedule is
- * also timed with runs sorted by output row (interleaved and contiguous XCD
- * placement, cwlb_ctx_set_locality), the winner is kept on the context and
- * written there (1, 0 or the context's previous setting = task order kept);
+ * timed afresh under the context's placement and with runs sorted by output
+ * row (interleaved and contiguous XCD placement, cwlb_ctx_set_locality), in
+ * two interleaved rounds; the winner is kept on the context and written
+ * there (the context's previous setting when it wins);
  * then with the occupancy variant (cwlb_ctx_set_occupancy, kept when
  * faster, and then also timed at half and double the run length, so the
  * tasks per wave returned can be 1); then with cache hints of 24, 48 and
