@@ -185,12 +185,13 @@ SingleSResult run_single_s(cwlb::Device& queue, const CSR_Order& csr,
     // The launch schedule for this graph and S, timed once before the timed
     // launches like the S search itself (cwlb_ctx_tune_schedule), unless
     // CWLB_TUNE_SCHEDULE=0 keeps the automatic schedule.  Both start from
-    // the automatic schedule in task order with the standard kernel and no
-    // cache hints, so every S is treated alike.
+    // the automatic schedule in task order with the standard kernel, no
+    // cache hints and one pass, so every S is treated alike.
     cwlb::check(cwlb_ctx_set_schedule(queue.ctx(), 0, 0), "cwlb_ctx_set_schedule");
     cwlb::check(cwlb_ctx_set_locality(queue.ctx(), 0, 0), "cwlb_ctx_set_locality");
     cwlb::check(cwlb_ctx_set_cache_hints(queue.ctx(), 0), "cwlb_ctx_set_cache_hints");
     cwlb::check(cwlb_ctx_set_occupancy(queue.ctx(), 0), "cwlb_ctx_set_occupancy");
+    cwlb::check(cwlb_ctx_set_column_phases(queue.ctx(), 0), "cwlb_ctx_set_column_phases");
     const char* tune_env = std::getenv("CWLB_TUNE_SCHEDULE");
     const bool tune = !(tune_env && std::string(tune_env) == "0");
     if (tune && !tasks.empty() && K > 0) {
@@ -208,6 +209,8 @@ SingleSResult run_single_s(cwlb::Device& queue, const CSR_Order& csr,
                     "cwlb_ctx_get_cache_hints");
         cwlb::check(cwlb_ctx_get_occupancy(queue.ctx(), &result.waves_per_simd),
                     "cwlb_ctx_get_occupancy");
+        cwlb::check(cwlb_ctx_get_column_phases(queue.ctx(), &result.column_phases),
+                    "cwlb_ctx_get_column_phases");
     }
 
     const std::string device_name = queue.name();

@@ -75,6 +75,8 @@ struct SingleSResult {
     std::int64_t cache_hint_bytes = 0;
     // 6 when the timed launches ran the occupancy variant, else 0.
     std::int32_t waves_per_simd = 0;
+    // Column phases the timed launches ran with (0 = one pass).
+    std::int32_t column_phases = 0;
 };
 
 // Builds the tasks for S (on the GPU, identical to the host partition), then
