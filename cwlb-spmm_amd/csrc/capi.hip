@@ -356,8 +356,9 @@ cwlb_status cwlb_ctx_device_info(cwlb_ctx* ctx, cwlb_device_info* out)
 cwlb_status cwlb_ctx_set_schedule(cwlb_ctx* ctx, int32_t tasks_per_wave, int32_t feature_slices)
 {
     if (!ctx) return fail(CWLB_INVALID_ARG, "null context");
-    if (tasks_per_wave < 0)
-        return fail(CWLB_INVALID_ARG, "tasks_per_wave must be >= 0 (0 = automatic)");
+    if (tasks_per_wave < 0 || tasks_per_wave > (1 << 20))
+        return fail(CWLB_INVALID_ARG,
+                    "tasks_per_wave must be in [0, 1048576] (0 = automatic)");
     if (feature_slices != 0 && feature_slices != 1 && feature_slices != 2 && feature_slices != 4 &&
         feature_slices != 8)
         return fail(CWLB_INVALID_ARG, "feature_slices must be 0, 1, 2, 4 or 8");

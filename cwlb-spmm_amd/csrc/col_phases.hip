@@ -44,8 +44,9 @@ phase_bounds(const int* __restrict__ rp, const int* __restrict__ ci, int n_rows,
         const bool ok = p0 >= 0 && p1 >= p0 && static_cast<long long>(p1) <= nnz;
         int cnt = 0;
         if (ok) {
-            for (int j0 = p0; j0 < p1; j0 += 64) {
-                const int j = j0 + lane;
+            // (64-bit steps: a row may end within 64 of 2^31)
+            for (long long j0 = p0; j0 < p1; j0 += 64) {
+                const long long j = j0 + lane;
                 int band = P;  // past the row: below no bound
                 if (j < p1) {
                     const int c = ci[j];

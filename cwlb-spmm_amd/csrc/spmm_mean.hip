@@ -480,7 +480,9 @@ spmm_mean_runs(const int* __restrict__ rp, const int* __restrict__ ci,
                     V acc[R];
 #pragma unroll
                     for (int q = 0; q < R; ++q) acc[q] = vzero<VEC>();
-                    for (int w0 = c0.b; w0 < c0.e; w0 += 64) {
+                    // (an unsigned step: a chunk may end within 64 of 2^31)
+                    for (unsigned uw = c0.b; uw < static_cast<unsigned>(c0.e); uw += 64u) {
+                        const int w0 = static_cast<int>(uw);
                         const int wn = min(64, c0.e - w0);
                         const int lane = fresh(threadIdx.x & 63);
                         int colw = 0;

@@ -103,8 +103,8 @@ cwlb_status cwlb_ctx_set_stream(cwlb_ctx* ctx, void* stream);
 cwlb_status cwlb_ctx_synchronize(cwlb_ctx* ctx);
 cwlb_status cwlb_ctx_device_info(cwlb_ctx* ctx, cwlb_device_info* out);
 /* Schedule of later SpMM calls on this context: tasks executed per wave
- * (a run of consecutive tasks) and feature slices spread across the XCDs.
- * 0 selects automatically (the default).  feature_slices must be 0, 1, 2, 4
+ * (a run of consecutive tasks, at most 2^20) and feature slices spread
+ * across the XCDs.  0 selects automatically (the default).  feature_slices must be 0, 1, 2, 4
  * or 8; the slices are whole 4-float vectors, as even as K allows (K = 600
  * in 4 slices: 38, 38, 37 and 37 vectors).  K not a multiple of 4, fewer
  * vectors than slices, or misaligned H / C fall back to 1 slice.

@@ -915,10 +915,11 @@ def test_fresh_context_defaults_and_last_launch(gpu_ctx):
 
 
 def test_schedule_and_locality_arguments(gpu_ctx):
-    for bad in ((-1, 0), (0, 3), (0, 16)):
+    for bad in ((-1, 0), (0, 3), (0, 16), ((1 << 20) + 1, 0)):
         with pytest.raises(capi.CwlbError) as e:
             gpu_ctx.set_schedule(*bad)
         assert e.value.status == capi.INVALID_ARG
+    gpu_ctx.set_schedule(1 << 20, 0)
     for bad in ((3, 0), (-1, 0), (0, 3), (0, -2)):
         with pytest.raises(capi.CwlbError) as e:
             gpu_ctx.set_locality(*bad)
@@ -937,12 +938,14 @@ def test_schedule_and_locality_arguments(gpu_ctx):
 MB = 1 << 20
 # Launch schedules checked at full size, per workload, as
 # (segment-size candidate index, tasks per wave, feature slices, run order,
-# XCD placement, hot-set bytes, waves per SIMD, flags); None = the schedule
-# cwlb_ctx_tune_schedule picks, which is what bench.py times.  The first
-# R-MAT entry is the headline launch of the benchmark (64 tasks per wave,
-# 2 feature slices, 48 MB cache hints, the standard kernel) at every
-# candidate S; the mesh and SBM entries are the launches their tuner kept
-# (runs by output row, contiguous XCD stretches, the occupancy variant).
+# XCD placement, hot-set bytes, waves per SIMD, flags[, column phases]);
+# None = the schedule cwlb_ctx_tune_schedule picks, which is what bench.py
+# times.  The first R-MAT entry is the headline launch of the benchmark (64
+# tasks per wave, 2 feature slices, 48 MB cache hints, the standard kernel)
+# at every candidate S; the mesh entries are the launches its tuner kept
+# (runs by output row, contiguous XCD stretches, the occupancy variant); the
+# SBM's phased entries are its tuner's launch (12 phases, 8 slices) and the
+# best point of a phase sweep in task order (16 phases, 4 slices).
 FULL_LAUNCHES = {
     4: [(0, 64, 2, 1, 1, 48 * MB, 0, 0), (2, 64, 2, 1, 1, 48 * MB, 0, 0),
         (2, 64, 4, 1, 1, 0, 6, 0), (1, 64, 2, 1, 1, 48 * MB, 0, 0),
