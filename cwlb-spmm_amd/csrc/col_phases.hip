@@ -116,6 +116,9 @@ cwlb_status build_column_phases(cwlb_ctx* ctx, const SpmmArgs& a, int phases, bo
     const cwlb_status s = launch_phase_bounds(ctx->stream, a.row_ptr, a.col_idx, a.n_rows, a.nnz,
                                               a.h_rows, phases, ctx->d_phase_bounds);
     if (s != CWLB_OK) return s;
+    // The bounds are complete before any stream can use them (the context's
+    // stream may be switched before the next call).
+    CWLB_HIP_TRY(hipStreamSynchronize(ctx->stream));
     ctx->phase_rp = a.row_ptr;
     ctx->phase_col = a.col_idx;
     ctx->phase_n_rows = a.n_rows;

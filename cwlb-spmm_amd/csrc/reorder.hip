@@ -260,6 +260,9 @@ cwlb_status build_run_order(cwlb_ctx* ctx, const SpmmArgs& a, int M, long long n
     CWLB_HIP_TRY(rocprim::radix_sort_pairs(ctx->d_sort_temp, bytes, ctx->d_run_keys,
                                            ctx->d_run_keys_sorted, ids, ctx->d_run_order, n_runs,
                                            0u, end_bit, st));
+    // The order is complete before any stream can use it (the context's
+    // stream may be switched before the next call).
+    CWLB_HIP_TRY(hipStreamSynchronize(st));
     ctx->order_tasks = a.tasks;
     ctx->order_origin = a.origin;
     ctx->order_n_tasks = a.n_tasks;

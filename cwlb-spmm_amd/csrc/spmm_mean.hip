@@ -1184,6 +1184,10 @@ cwlb_status launch_spmm_mean(cwlb_ctx* ctx, const SpmmArgs& a, bool zero_all, bo
         if (s != CWLB_OK) return s;
     }
     ctx->last_call_hinted = p.hints != nullptr;
+    if (p.ordered && a.n_tasks > 0 && a.K > 0) {
+        const cwlb_status s = build_run_order(ctx, a, p.M, p.runs, may_build, &p.order);
+        if (s != CWLB_OK) return s;
+    }
     if (record_events) CWLB_HIP_TRY(hipEventRecord(ctx->ev[0], st));
     const long long total = static_cast<long long>(a.n_rows) * a.K;
     if (zero_all) {
@@ -1192,10 +1196,6 @@ cwlb_status launch_spmm_mean(cwlb_ctx* ctx, const SpmmArgs& a, bool zero_all, bo
             static_cast<unsigned>(std::max<long long>(1, std::min<long long>(want, 65536)));
         hipLaunchKernelGGL(fill_zero, dim3(blocks), dim3(kBlock), 0, st, a.C,
                            std::max<long long>(total, 0), ctx->d_status);
-    }
-    if (p.ordered && a.n_tasks > 0 && a.K > 0) {
-        const cwlb_status s = build_run_order(ctx, a, p.M, p.runs, may_build, &p.order);
-        if (s != CWLB_OK) return s;
     }
     ctx->last_launch.tasks_per_wave = p.M;
     ctx->last_launch.feature_slices = p.sl;

@@ -115,7 +115,8 @@ cwlb_status cwlb_ctx_set_schedule(cwlb_ctx* ctx, int32_t tasks_per_wave, int32_t
 /* Locality of later SpMM calls on this context.  run_order: 0 automatic,
  * 1 runs in task order, 2 runs sorted by the original id of their first row
  * (a device sort, redone only when the task array, origin array, task count
- * or run length changes; it groups the rows of all degree classes that
+ * or run length changes, by a call that then synchronises its stream; it
+ * groups the rows of all degree classes that
  * neighbour each other in the original numbering.  Every order of the runs
  * gives the same result, so after rewriting a task array in place only the
  * speed can suffer; calling this function again forces a new sort).
@@ -169,8 +170,8 @@ cwlb_status cwlb_ctx_get_occupancy(cwlb_ctx* ctx, int32_t* waves_per_simd);
  * 480 nonzeros per row and K = 600, 16 phases, 15% faster).  The per-row
  * bounds of the passes (P - 1 ints per row, see cwlb_column_phase_bounds)
  * are built by the first call after a change of the row or column array,
- * n_rows, nnz, h_rows or P into a context-owned buffer (no
- * synchronisation) and reused later; under graph capture they are only
+ * n_rows, nnz, h_rows or P into a context-owned buffer (that call
+ * synchronises its stream) and reused later; under graph capture they are only
  * reused (otherwise the call runs in one pass).  Any bounds give the same
  * result, so bounds left over from earlier array contents only cost speed.
  * Applies to task lists that are chains -- every task well formed and

@@ -376,3 +376,37 @@ def test_tuner_tries_phases(gpu_ctx, reset):
     np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-6)
     del H, C
     torch.cuda.empty_cache()
+
+
+def test_stream_switch_after_builds(gpu_ctx, reset):
+    """The run order and the phase bounds built by an asynchronous call on
+    one stream serve a call on another stream right after (the building
+    call synchronises its stream)."""
+    torch = torch_mod()
+    g = workloads.small(4, seed=12)
+    K = 64
+    p = problem(g, SKEWED_COSTS, 7)
+    d_rp, d_ci, d_v, d_o = dev(p.row_ptr), dev(p.col_idx), dev(p.val), dev(p.origin)
+    d_t = dev(np.ascontiguousarray(p.tasks).reshape(-1))
+    H = synth.features(g.n, K, 8)
+    d_H = dev(H)
+    ref = oracle.spmm_mean_f32(p.row_ptr, p.col_idx, p.val, p.origin, H, p.tasks)
+    a, b = torch.cuda.Stream(), torch.cuda.Stream()
+    Ca = torch.zeros((g.n, K), dtype=torch.float32, device="cuda")
+    Cb = torch.zeros_like(Ca)
+    torch.cuda.synchronize()
+    set_phased(gpu_ctx, 7, 4, 2, order=2, xcd=2)
+    try:
+        gpu_ctx.set_stream(a.cuda_stream)
+        gpu_ctx.spmm(d_rp, d_ci, d_v, d_o, g.n, g.nnz, d_H, g.n, K, d_t, len(p.tasks), Ca,
+                     timed=False)
+        gpu_ctx.set_stream(b.cuda_stream)
+        gpu_ctx.spmm(d_rp, d_ci, d_v, d_o, g.n, g.nnz, d_H, g.n, K, d_t, len(p.tasks), Cb,
+                     timed=False)
+        info = gpu_ctx.last_launch()
+        torch.cuda.synchronize()
+    finally:
+        gpu_ctx.set_stream(torch.cuda.current_stream().cuda_stream)
+    assert (info["column_phases"], info["run_order"]) == (7, 2), info
+    check(Ca.cpu().numpy(), ref)
+    check(Cb.cpu().numpy(), ref)
