@@ -312,7 +312,8 @@ cwlb_status cwlb_ctx_destroy(cwlb_ctx* ctx)
     for (void* p : {static_cast<void*>(ctx->d_run_keys), static_cast<void*>(ctx->d_run_keys_sorted),
                     static_cast<void*>(ctx->d_run_order), ctx->d_sort_temp,
                     static_cast<void*>(ctx->d_col_counts), static_cast<void*>(ctx->d_count_hist),
-                    static_cast<void*>(ctx->d_hints), static_cast<void*>(ctx->d_phase_bounds)})
+                    static_cast<void*>(ctx->d_hints), static_cast<void*>(ctx->d_phase_bounds),
+                    static_cast<void*>(ctx->d_band_col), static_cast<void*>(ctx->d_band_val)})
         if (p) (void)hipFree(p);
     for (void* p : ctx->retired) (void)hipFree(p);
     for (int b = 0; b < 2; ++b) {
@@ -430,20 +431,25 @@ cwlb_status cwlb_ctx_get_column_phases(cwlb_ctx* ctx, int32_t* phases)
 }
 
 cwlb_status cwlb_column_phase_bounds(cwlb_ctx* ctx, const int32_t* row_ptr,
-                                     const int32_t* col_idx, int32_t n_rows, int64_t nnz,
-                                     int64_t h_rows, int32_t phases, int32_t* out)
+                                     const int32_t* col_idx, const float* val, int32_t n_rows,
+                                     int64_t nnz, int64_t h_rows, int32_t phases,
+                                     int32_t* bounds_out, int32_t* col_out, float* val_out)
 {
     if (!ctx) return fail(CWLB_INVALID_ARG, "null context");
     if (phases < 2 || phases > 64)
         return fail(CWLB_INVALID_ARG, "cwlb_column_phase_bounds: phases must be in [2, 64]");
-    if (n_rows < 0 || nnz < 0 || h_rows <= 0)
+    if (n_rows < 0 || nnz < 0 || nnz > INT32_MAX || h_rows <= 0)
+        return fail(CWLB_INVALID_ARG, "cwlb_column_phase_bounds: n_rows >= 0, 0 <= nnz < 2^31 "
+                                      "and h_rows > 0 required");
+    if (!col_out != !val_out)
         return fail(CWLB_INVALID_ARG,
-                    "cwlb_column_phase_bounds: n_rows >= 0, nnz >= 0 and h_rows > 0 required");
-    if (n_rows > 0 && (!row_ptr || !out || (nnz > 0 && !col_idx)))
+                    "cwlb_column_phase_bounds: col_out and val_out go together");
+    if (n_rows > 0 && (!row_ptr || (nnz > 0 && (!col_idx || (col_out && !val)))))
         return fail(CWLB_INVALID_ARG, "cwlb_column_phase_bounds: null array");
     DeviceGuard g(ctx->device);
     (void)hipGetLastError();
-    return launch_phase_bounds(ctx->stream, row_ptr, col_idx, n_rows, nnz, h_rows, phases, out);
+    return launch_phase_bounds(ctx->stream, row_ptr, col_idx, val, n_rows, nnz, h_rows, phases,
+                               bounds_out, col_out, val_out);
 }
 
 cwlb_status cwlb_ctx_last_launch(cwlb_ctx* ctx, cwlb_launch_info* out)
@@ -653,7 +659,7 @@ cwlb_status cwlb_ctx_tune_schedule(cwlb_ctx* ctx, const int32_t* row_ptr, const 
         // (>= 512 MB) and rows of 64 nonzeros or more on average (each
         // phase reads and writes C once).  8, 12 and 16 phases, each with
         // every slice count whose widest slice fits one vector per lane,
-        // at 16 and 64 tasks per wave, under the placement chosen above;
+        // at 16, 32 and 64 tasks per wave, under the placement chosen above;
         // kept when faster than the settings so far, re-timed first.
         const long long h_bytes = h_rows * static_cast<long long>(K) * 4;
         if (st == CWLB_OK && h_bytes >= (512ll << 20) && nnz >= 64ll * n_rows && K % 4 == 0) {
@@ -664,7 +670,7 @@ cwlb_status cwlb_ctx_tune_schedule(cwlb_ctx* ctx, const int32_t* row_ptr, const 
             for (int P : {8, 12, 16}) {
                 for (int sl : {1, 2, 4, 8}) {
                     if (K / 4 < sl || (K / 4 + sl - 1) / sl > 64) continue;
-                    for (int m : {16, 64}) {
+                    for (int m : {16, 32, 64}) {
                         if (st != CWLB_OK) break;
                         ctx->sched_phases = P;
                         ctx->sched_slices = sl;

@@ -74,18 +74,17 @@ struct cwlb_ctx {
     unsigned hint_theta = 0;
     bool hint_any_cold = false;
     bool last_call_hinted = false;  // the last aggregation launch used hints
-    // Column phases (0 or 1 = none): the P - 1 interior row bounds, P - 1
-    // arrays of n_rows ints, with what they were built for, and the
-    // sequence number of the last phased call.
+    // Column phases (0 or 1 = none): grow-only buffers that each phased call
+    // rewrites -- the P - 1 interior row bounds (P - 1 arrays of n_rows
+    // ints) and the band-sorted copy of the column and value arrays -- and
+    // the sequence number of the last phased call.
     int sched_phases = 0;
     int* d_phase_bounds = nullptr;
     long long phase_cap = 0;
-    const void* phase_rp = nullptr;
-    const void* phase_col = nullptr;
-    long long phase_n_rows = -1;
-    long long phase_nnz = -1;
-    long long phase_h_rows = -1;
-    int phase_P = 0;
+    int* d_band_col = nullptr;
+    long long band_cap_col = 0;
+    float* d_band_val = nullptr;
+    long long band_cap_val = 0;
     int phase_seq = 0;
     cwlb_launch_info last_launch{};  // the last aggregation launch's schedule
     // Pinned host staging of the host-pointer entry point: two buffers used
@@ -173,16 +172,25 @@ cwlb_status launch_fill_features(cwlb_ctx* ctx, float* H, int64_t rows, int32_t 
 cwlb_status build_cache_hints(cwlb_ctx* ctx, const SpmmArgs& a, long long hot_rows,
                               bool may_build, const unsigned long long** hints);
 
-// Builds (or reuses) the row bounds of `phases` column phases
-// (csrc/col_phases.hip) on ctx->stream.  *bounds is null when they would
-// have to be built but may_build is false (a stream under graph capture).
-cwlb_status build_column_phases(cwlb_ctx* ctx, const SpmmArgs& a, int phases, bool may_build,
-                                const int** bounds);
+// The context buffers of a column-phased call.
+struct PhaseArrays {
+    int32_t* bounds = nullptr;  // (P - 1) x n_rows
+    int32_t* col = nullptr;     // nnz, each row's nonzeros sorted by band
+    float* val = nullptr;       // nnz, likewise
+};
 
-// Enqueues the bounds kernel: out[(p - 1) * n_rows + r] for p in [1, phases).
+// Sizes the context's phase buffers for `phases` column phases
+// (csrc/col_phases.hip); all null when they cannot be used (a stream under
+// graph capture, where nothing is allocated, and buffers too small).
+cwlb_status prepare_column_phases(cwlb_ctx* ctx, const SpmmArgs& a, int phases, bool may_build,
+                                  PhaseArrays* out);
+
+// Enqueues the band sort: bounds[(p - 1) * n_rows + r] for p in [1, phases)
+// (bounds may be null) and, when col_out is non-null, the band-sorted copy
+// of col_idx and val.
 cwlb_status launch_phase_bounds(hipStream_t st, const int32_t* row_ptr, const int32_t* col_idx,
-                                int32_t n_rows, int64_t nnz, int64_t h_rows, int phases,
-                                int32_t* out);
+                                const float* val, int32_t n_rows, int64_t nnz, int64_t h_rows,
+                                int phases, int32_t* bounds, int32_t* col_out, float* val_out);
 
 cwlb_status launch_reorder(cwlb_ctx* ctx, int32_t n_rows, int64_t nnz, const int32_t* row_ptr,
                            const int32_t* col_idx, const float* val, int32_t* origin,

@@ -370,10 +370,11 @@ __device__ __forceinline__ void block_slice(int& slice, long long& jb, long long
                    : static_cast<long long>(bx >> 3) * P + q;
 }
 
-// PH: one launch of a column-phased call (pb, pe: this phase's row bounds,
-// first: the first phase, seq: the call's sequence number; status[1] ==
-// seq marks a task list that is not a chain, which then runs unphased in
-// the first launch and not at all in the others).
+// PH: one launch of a column-phased call (pb, pe: this phase's row bounds
+// in ci_b / val_b, the copy of ci / val with each row's nonzeros sorted by
+// band; first: the first phase; seq: the call's sequence number; status[1]
+// == seq marks a task list that is not a chain, which then runs in one pass
+// over ci / val in the first launch and not at all in the others).
 template <int VEC, int G, int R, int U, int SL, bool HN, bool O6, bool PH>
 __global__ void __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(O6 ? 6 : 1)))
 spmm_mean_runs(const int* __restrict__ rp, const int* __restrict__ ci,
@@ -383,7 +384,8 @@ spmm_mean_runs(const int* __restrict__ rp, const int* __restrict__ ci,
                long long n_blocks, long long chunk, const int* __restrict__ run_order,
                const unsigned long long* __restrict__ hints, float* __restrict__ C,
                int* __restrict__ status, const int* __restrict__ pb,
-               const int* __restrict__ pe, int first_phase, int seq)
+               const int* __restrict__ pe, const int* __restrict__ ci_b,
+               const float* __restrict__ val_b, int first_phase, int seq)
 {
     static_assert(!HN || VEC == 4, "hinted gathers move 16 bytes per lane");
     using V = typename VecT<VEC>::T;
@@ -444,8 +446,13 @@ spmm_mean_runs(const int* __restrict__ rp, const int* __restrict__ ci,
     if constexpr (HN) hrsrc = feature_rsrc(H, h_rows, ld);
     const unsigned slice_bytes = static_cast<unsigned>(f0 * VEC) * 4u;
 
-    // One segment: task (rs, re, fo, ln).
-    auto run_segment = [&](const int rs, const int re, const int fo, const int ln) {
+    // One segment: task (rs, re, fo, ln) over the column and value arrays
+    // cx / vx; banded: the rows are whole rows of a chain, read band by band
+    // from the sorted copy under column phases.
+    auto run_segment = [&](const int rs, const int re, const int fo, const int ln,
+                           const int* __restrict__ cx, const float* __restrict__ vx,
+                           const bool banded) {
+        const bool bph = PH && ph && banded;
         const int rlo = max(rs, 0);
         const int rhi = min(re, n_rows);
         for (int pass = 0; pass < npass; ++pass) {
@@ -465,14 +472,14 @@ spmm_mean_runs(const int* __restrict__ rp, const int* __restrict__ ci,
                 Chunk my = {0, 0, 0, 0};
                 Chunk c0;
                 if constexpr (kEarly) {
-                    if (mine) my = task_chunk<PH>(rp, rr, rs, re, fo, ln, nnz, ph, pb, pe);
+                    if (mine) my = task_chunk<PH>(rp, rr, rs, re, fo, ln, nnz, bph, pb, pe);
                     c0.base = __builtin_amdgcn_readfirstlane(my.base);
                     c0.b = __builtin_amdgcn_readfirstlane(my.b);
                     c0.e = __builtin_amdgcn_readfirstlane(my.e);
                     c0.d = __builtin_amdgcn_readfirstlane(my.d);
                     if constexpr (PH) c0.own = __builtin_amdgcn_readfirstlane(my.own);
                 } else {
-                    c0 = task_chunk<PH>(rp, r, rs, re, fo, ln, nnz, ph, pb, pe);
+                    c0 = task_chunk<PH>(rp, r, rs, re, fo, ln, nnz, bph, pb, pe);
                 }
                 const int len0 = c0.e - c0.b;
                 if (len0 >= kLong) {
@@ -488,8 +495,8 @@ spmm_mean_runs(const int* __restrict__ rp, const int* __restrict__ ci,
                         int colw = 0;
                         float valw = 0.0f;
                         if (lane < wn) {
-                            colw = __builtin_nontemporal_load(ci + c0.base + w0 + lane);
-                            valw = __builtin_nontemporal_load(val + c0.base + w0 + lane);
+                            colw = __builtin_nontemporal_load(cx + c0.base + w0 + lane);
+                            valw = __builtin_nontemporal_load(vx + c0.base + w0 + lane);
                             if constexpr (HN) colw = with_hint(colw, hints, c0.base + w0 + lane);
                         }
                         for (int k0 = 0; k0 < wn; k0 += STEP) {
@@ -551,7 +558,7 @@ spmm_mean_runs(const int* __restrict__ rp, const int* __restrict__ ci,
                     } else if (slot == 0) {
                         float* crow = Cs + static_cast<size_t>(o) * ld;
                         const float fd = static_cast<float>(c0.d);
-                        const int how = write_mode<PH>(ph, first, c0);
+                        const int how = write_mode<PH>(bph, first, c0);
 #pragma unroll
                         for (int q = 0; q < R; ++q) {
                             const int f = fl + G * q;
@@ -565,7 +572,7 @@ spmm_mean_runs(const int* __restrict__ rp, const int* __restrict__ ci,
                 // ---------------- short rows: one row per slot, RU rows per slot
                 const int lane = lane_g;
                 if constexpr (!kEarly) {
-                    if (mine) my = task_chunk<PH>(rp, rr, rs, re, fo, ln, nnz, ph, pb, pe);
+                    if (mine) my = task_chunk<PH>(rp, rr, rs, re, fo, ln, nnz, bph, pb, pe);
                 }
                 const int mylen = my.e - my.b;
                 // The group: the leading rows that are short, start where the
@@ -602,8 +609,8 @@ spmm_mean_runs(const int* __restrict__ rp, const int* __restrict__ ci,
 #pragma unroll
                     for (int t = 0; t < NT; ++t) {
                         const int i = lane + 64 * t;
-                        lc[t] = i < gn ? __builtin_nontemporal_load(ci + gs + i) : 0;
-                        lv[t] = i < gn ? __builtin_nontemporal_load(val + gs + i) : 0.0f;
+                        lc[t] = i < gn ? __builtin_nontemporal_load(cx + gs + i) : 0;
+                        lv[t] = i < gn ? __builtin_nontemporal_load(vx + gs + i) : 0.0f;
                         if constexpr (HN)
                             if (i < gn) lc[t] = with_hint(lc[t], hints, gs + i);
                     }
@@ -619,8 +626,8 @@ spmm_mean_runs(const int* __restrict__ rp, const int* __restrict__ ci,
                     __builtin_amdgcn_wave_barrier();
                     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
                 } else if (lane < gn) {
-                    colw = __builtin_nontemporal_load(ci + gs + lane);
-                    valw = __builtin_nontemporal_load(val + gs + lane);
+                    colw = __builtin_nontemporal_load(cx + gs + lane);
+                    valw = __builtin_nontemporal_load(vx + gs + lane);
                     if constexpr (HN) colw = with_hint(colw, hints, gs + lane);
                 }
                 V acc[RU][R];
@@ -715,11 +722,11 @@ spmm_mean_runs(const int* __restrict__ rp, const int* __restrict__ ci,
                                     if (f < F) vstore_nt<VEC>(crow + f * VEC, vzero<VEC>());
                                 }
                             }
-                        } else if (cu.e > cu.b || (PH && ph && first && cu.own)) {
+                        } else if (cu.e > cu.b || (bph && first && cu.own)) {
                             // (an owned row with no nonzero in the first phase
                             // is stored as zeros all the same)
                             const float fd = static_cast<float>(cu.d);
-                            const int how = write_mode<PH>(ph, first, cu);
+                            const int how = write_mode<PH>(bph, first, cu);
 #pragma unroll
                             for (int q = 0; q < R; ++q) {
                                 const int f = fl + G * q;
@@ -751,9 +758,39 @@ spmm_mean_runs(const int* __restrict__ rp, const int* __restrict__ ci,
             const cwlb_task zl = tasks[n_tasks - 1];
             const bool head = t0 == 0;
             const int rs = (head || a.first_row_offset == 0) ? a.row_start : a.row_start + 1;
+            const int re = z.row_end;
             const int fo = head ? a.first_row_offset : 0;
-            const int ln = z.row_end == zl.row_end ? zl.last_row_nnz : 0;
-            if (rs < z.row_end) run_segment(rs, z.row_end, fo, ln);
+            const int ln = re == zl.row_end ? zl.last_row_nnz : 0;
+            if (rs < re) {
+                // Task offsets index the caller's order of a row's nonzeros:
+                // the rows the chain covers only in part (its first row when
+                // it starts inside it, its last when it ends at an offset)
+                // are summed whole from ci / val in the first phase; the
+                // others band by band from the sorted copy.
+                const int bs = rs + (fo > 0 ? 1 : 0);
+                const int be = max(bs, re - (ln > 0 ? 1 : 0));
+                for (int piece = 0; piece < 3; ++piece) {
+                    int s = bs, e = be, pfo = 0, pln = 0;
+                    bool banded = true;
+                    if (piece == 1) {  // the first row, from offset fo
+                        if (!first || fo == 0) continue;
+                        s = rs;
+                        e = rs + 1;
+                        pfo = fo;
+                        pln = (ln > 0 && re == rs + 1) ? ln : 0;
+                        banded = false;
+                    } else if (piece == 2) {  // the last row, up to offset ln
+                        if (!first || ln == 0 || (fo > 0 && re == rs + 1)) continue;
+                        s = re - 1;
+                        e = re;
+                        pln = ln;
+                        banded = false;
+                    }
+                    if (s < e)
+                        run_segment(s, e, pfo, pln, banded ? ci_b : ci, banded ? val_b : val,
+                                    banded);
+                }
+            }
             if (bad) atomicOr(status, bad);
             return;
         }
@@ -778,7 +815,8 @@ spmm_mean_runs(const int* __restrict__ rp, const int* __restrict__ ci,
             const int e0 = rest ? __builtin_ctzll(rest) : wn;
             const cwlb_task a = tasks[tw + s0];
             const cwlb_task z = tasks[tw + e0 - 1];
-            run_segment(a.row_start, z.row_end, a.first_row_offset, z.last_row_nnz);
+            run_segment(a.row_start, z.row_end, a.first_row_offset, z.last_row_nnz, ci, val,
+                        false);
         } while (rest);
     }
     if (bad) atomicOr(status, bad);
@@ -926,6 +964,8 @@ struct Plan {
     // whether it is the first, and the call's sequence number.
     const int* pb;
     const int* pe;
+    const int* cb;    // the band-sorted copy of the columns
+    const float* vb;  // and of the values
     int first;
     int seq;
 };
@@ -950,7 +990,7 @@ int launch_main(hipStream_t st, const SpmmArgs& a, const Plan& p, int* status)
                        a.col_idx, a.val, a.origin, a.n_rows, static_cast<long long>(a.nnz), a.H,
                        static_cast<long long>(a.h_rows), a.K, a.tasks,
                        static_cast<long long>(a.n_tasks), p.M, p.runs, p.blocks, p.chunk, p.order,
-                       p.hints, a.C, status, p.pb, p.pe, p.first, p.seq);
+                       p.hints, a.C, status, p.pb, p.pe, p.cb, p.vb, p.first, p.seq);
     return waves_per_cu;
 }
 
@@ -1135,6 +1175,8 @@ Plan make_plan(const cwlb_ctx* ctx, const SpmmArgs& a, bool per_task)
     }
     p.pb = nullptr;
     p.pe = nullptr;
+    p.cb = nullptr;
+    p.vb = nullptr;
     p.first = 1;
     p.seq = 0;
     return p;
@@ -1162,14 +1204,15 @@ cwlb_status launch_spmm_mean(cwlb_ctx* ctx, const SpmmArgs& a, bool zero_all, bo
     CWLB_HIP_TRY(hipStreamIsCapturing(st, &capture));
     const bool may_build = capture == hipStreamCaptureStatusNone;
     const bool work = a.n_tasks > 0 && a.K > 0;
-    // Column phases: the row bounds of the phases (built, or reused under
-    // capture; without them the call runs unphased, with the same result).
-    const int* bounds = nullptr;
+    // Column phases: the context's buffers for the band sort (under capture
+    // only when an earlier call sized them; without them the call runs in
+    // one pass, with the same result).
+    PhaseArrays ph_arr;
     if (p.phases > 1 && work) {
-        const cwlb_status s = build_column_phases(ctx, a, p.phases, may_build, &bounds);
+        const cwlb_status s = prepare_column_phases(ctx, a, p.phases, may_build, &ph_arr);
         if (s != CWLB_OK) return s;
     }
-    if (!bounds) p.phases = 1;
+    if (!ph_arr.bounds) p.phases = 1;
     if (p.phases > 1) {
         ctx->phase_seq = ctx->phase_seq >= 0x7fffffff ? 1 : ctx->phase_seq + 1;
         p.seq = ctx->phase_seq;
@@ -1207,7 +1250,14 @@ cwlb_status launch_spmm_mean(cwlb_ctx* ctx, const SpmmArgs& a, bool zero_all, bo
     ctx->last_launch.grid_blocks = a.n_tasks > 0 && a.K > 0 ? p.grid : 0;
     ctx->last_launch.max_waves_per_cu = 0;
     ctx->last_launch.column_phases = p.phases;
-    // A phased call always runs the clearing pass: it also checks the chain.
+    // A phased call sorts each row's nonzeros by band into the context's
+    // copy, and always runs the clearing pass: it also checks the chain.
+    if (p.phases > 1) {
+        const cwlb_status s =
+            launch_phase_bounds(st, a.row_ptr, a.col_idx, a.val, a.n_rows, a.nnz, a.h_rows,
+                                p.phases, ph_arr.bounds, ph_arr.col, ph_arr.val);
+        if (s != CWLB_OK) return s;
+    }
     if ((!zero_all || p.phases > 1) && work) {
         if (p.vec == 4) launch_zero<4>(st, a, p, ctx->d_status);
         else if (p.vec == 2) launch_zero<2>(st, a, p, ctx->d_status);
@@ -1219,12 +1269,14 @@ cwlb_status launch_spmm_mean(cwlb_ctx* ctx, const SpmmArgs& a, bool zero_all, bo
     if (record_events) CWLB_HIP_TRY(hipEventRecord(ctx->ev[1], st));
     if (work) {
         int waves = 0;
+        p.cb = ph_arr.col;
+        p.vb = ph_arr.val;
         for (int ph = 0; ph < p.phases; ++ph) {
             // Phase ph reads the bounds ph - 1 and ph of the P - 1 stored
             // per row (the row's own start and end at the outer phases).
             const long long n = a.n_rows;
-            p.pb = ph > 0 ? bounds + (ph - 1) * n : nullptr;
-            p.pe = ph < p.phases - 1 ? bounds + ph * n : nullptr;
+            p.pb = ph > 0 ? ph_arr.bounds + (ph - 1) * n : nullptr;
+            p.pe = ph < p.phases - 1 ? ph_arr.bounds + ph * n : nullptr;
             p.first = ph == 0;
             if (p.vec == 4) waves = dispatch_main<4>(st, a, p, ctx->d_status);
             else if (p.vec == 2) waves = dispatch_main<2>(st, a, p, ctx->d_status);

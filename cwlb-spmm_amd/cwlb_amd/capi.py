@@ -126,7 +126,7 @@ def lib():
         L.cwlb_ctx_get_occupancy.argtypes = [vp, C.POINTER(i32)]
         L.cwlb_ctx_set_column_phases.argtypes = [vp, i32]
         L.cwlb_ctx_get_column_phases.argtypes = [vp, C.POINTER(i32)]
-        L.cwlb_column_phase_bounds.argtypes = [vp, vp, vp, i32, i64, i64, i32, vp]
+        L.cwlb_column_phase_bounds.argtypes = [vp, vp, vp, vp, i32, i64, i64, i32, vp, vp, vp]
         L.cwlb_ctx_tune_schedule.argtypes = [vp, vp, vp, vp, vp, i32, i64, vp, i64, i32, vp, i64,
                                              vp, i32, C.POINTER(i32), C.POINTER(i32), vp]
         spmm = [vp, vp, vp, vp, vp, i32, i64, vp, i64, i32, vp, i64, vp, u32, C.POINTER(Timing)]
@@ -339,10 +339,12 @@ class Context:
         check(lib().cwlb_ctx_get_column_phases(self.h, C.byref(v)))
         return v.value
 
-    def column_phase_bounds(self, row_ptr, col_idx, n_rows, nnz, h_rows, phases, out):
+    def column_phase_bounds(self, row_ptr, col_idx, val, n_rows, nnz, h_rows, phases,
+                            bounds_out=None, col_out=None, val_out=None):
         """cwlb_column_phase_bounds on device tensors (enqueued on the stream)."""
-        check(lib().cwlb_column_phase_bounds(self.h, _ptr(row_ptr), _ptr(col_idx), int(n_rows),
-                                             int(nnz), int(h_rows), int(phases), _ptr(out)))
+        check(lib().cwlb_column_phase_bounds(self.h, _ptr(row_ptr), _ptr(col_idx), _ptr(val),
+                                             int(n_rows), int(nnz), int(h_rows), int(phases),
+                                             _ptr(bounds_out), _ptr(col_out), _ptr(val_out)))
 
     def tune_schedule(self, row_ptr, col_idx, val, origin, n_rows, nnz, H, h_rows, K, tasks,
                       n_tasks, C_out, trials=3, locality=False):

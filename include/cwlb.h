@@ -159,44 +159,52 @@ cwlb_status cwlb_ctx_get_occupancy(cwlb_ctx* ctx, int32_t* waves_per_simd);
 
 /* Column phases of later SpMM calls on this context.  phases = 0 or 1 (the
  * default): one pass.  phases = P in [2, 64]: the task list is executed P
- * times, pass p gathering only the nonzeros whose column lies in
- * [p * h_rows / P, (p + 1) * h_rows / P), so that the feature rows all
- * waves read at a time span 1/P of H and stay in the caches.  A row that
- * one stretch of consecutive tasks covers whole (see CWLB_SPMM_PER_TASK) is
- * stored in the first pass and added to in the others without atomics,
- * which reads and writes C P times: it pays when H is well beyond the
- * 256 MB Infinity Cache, the columns of a row are spread over H and rows
- * hold many more nonzeros than 2P (measured: a 240k-row block model with
- * 480 nonzeros per row and K = 600, 16 phases, 15% faster).  The per-row
- * bounds of the passes (P - 1 ints per row, see cwlb_column_phase_bounds)
- * are built by the first call after a change of the row or column array,
- * n_rows, nnz, h_rows or P into a context-owned buffer (that call
- * synchronises its stream) and reused later; under graph capture they are only
- * reused (otherwise the call runs in one pass).  Any bounds give the same
- * result, so bounds left over from earlier array contents only cost speed.
- * Applies to task lists that are chains -- every task well formed and
- * starting where its predecessor ended, as cwlb_partition's lists are --
- * which the device checks on every call; any other list runs in one pass.
- * Applies with 16-byte aligned H and C, K a multiple of 4 and at most 256
- * floats per feature slice, without CWLB_SPMM_PER_TASK; replaces the
- * occupancy variant and the cache hints while on.  Results agree with the
- * one-pass ones within the float tolerance (each phase's partial sum is
- * divided and added separately).  No counterpart in the reference;
- * cwlb_ctx_tune_schedule tries it. */
+ * times, pass p gathering only the nonzeros whose column c has
+ * c mod P = p, so that the feature rows all waves read at a time are 1/P of
+ * H and stay in the caches (the bands interleave the columns, so that
+ * communities numbered as ranges of ids spread over all passes).  Each
+ * phased call first writes, into context-owned buffers, a copy of col_idx
+ * and val with every row's nonzeros stably sorted by band and the row
+ * bounds of the bands (see cwlb_column_phase_bounds; 8 bytes per nonzero
+ * and 4 (P - 1) per row, kept and grown as needed; about 0.3 ms on a
+ * 115M-nonzero graph, reported in the timing's zero_us), so rewritten
+ * arrays are always read as they are.  A row that one stretch of
+ * consecutive tasks covers whole (see CWLB_SPMM_PER_TASK) is stored in the
+ * first pass and added to in the others without atomics, which reads and
+ * writes C P times: phases pay when H is well beyond the 256 MB Infinity
+ * Cache, the columns of a row are spread over H and rows hold many more
+ * nonzeros than 2P (measured: a 240k-row block model with 480 nonzeros per
+ * row and K = 600, 16 phases, 27% faster).  Under graph capture the
+ * buffers are only used when an earlier call sized them (otherwise the
+ * call runs in one pass); a buffer a capture used is never freed before
+ * cwlb_ctx_destroy.  Applies to task lists that are chains -- every task
+ * well formed and starting where its predecessor ended, as
+ * cwlb_partition's lists are -- which the device checks on every call; any
+ * other list runs in one pass (over the band-sorted copy).  Applies with
+ * 16-byte aligned H and C, K a multiple of 4 and at most 256 floats per
+ * feature slice, without CWLB_SPMM_PER_TASK; replaces the occupancy variant
+ * and the cache hints while on.  Results agree with the one-pass ones
+ * within the float tolerance (each row is summed band by band, each band's
+ * partial sum divided and added separately).  No counterpart in the
+ * reference; cwlb_ctx_tune_schedule tries it. */
 cwlb_status cwlb_ctx_set_column_phases(cwlb_ctx* ctx, int32_t phases);
 cwlb_status cwlb_ctx_get_column_phases(cwlb_ctx* ctx, int32_t* phases);
 
-/* The interior bounds of P column phases (2 <= P <= 64), enqueued on the
- * context's stream from device arrays: out[(p - 1) * n_rows + r] =
- * row_ptr[r] + the number of nonzeros of row r whose column c has
- * floor(c * P / h_rows) < p, for p in [1, P) (a column below 0 counts in
- * band 0, one at or above h_rows in band P - 1; a row whose offsets leave
- * [0, nnz] or decrease gets 0).  out holds (P - 1) * n_rows ints.  No
- * counterpart in the reference; the column-phased aggregation builds these
- * itself, tests read them here. */
+/* The band sort of P column phases (2 <= P <= 64), enqueued on the
+ * context's stream from device arrays.  The band of a column c is c mod P
+ * (a column below 0 or at or above h_rows is in band 0).  bounds_out
+ * (optional, (P - 1) * n_rows ints): bounds_out[(p - 1) * n_rows + r] =
+ * row_ptr[r] + the number of nonzeros of row r in bands below p, for p in
+ * [1, P).  col_out and val_out (optional, together, nnz each): col_idx and
+ * val with each row's nonzeros stably sorted by band, so that band p of
+ * row r is [B_p(r), B_{p+1}(r)) with B_0(r) = row_ptr[r] and B_P(r) =
+ * row_ptr[r + 1].  A row whose offsets leave [0, nnz] or decrease gets
+ * bounds 0 and is not copied.  No counterpart in the reference; the
+ * column-phased aggregation runs this itself, tests read it here. */
 cwlb_status cwlb_column_phase_bounds(cwlb_ctx* ctx, const int32_t* row_ptr,
-                                     const int32_t* col_idx, int32_t n_rows, int64_t nnz,
-                                     int64_t h_rows, int32_t phases, int32_t* out);
+                                     const int32_t* col_idx, const float* val, int32_t n_rows,
+                                     int64_t nnz, int64_t h_rows, int32_t phases,
+                                     int32_t* bounds_out, int32_t* col_out, float* val_out);
 
 /* The schedule the last aggregation launch on this context used, as the
  * automatic choices and the context's settings resolved it (all zero before
@@ -310,7 +318,7 @@ cwlb_status cwlb_spmm_mean_f32_large_k(cwlb_ctx* ctx, const int32_t* row_ptr,
  * again with those hints when the variant was kept; then, when H holds at
  * least 512 MB, K is a multiple of 4 and rows average 64 nonzeros or more,
  * with 8, 12 and 16 column phases (cwlb_ctx_set_column_phases) at every
- * slice count they take and 16 or 64 tasks per wave: the fastest is kept
+ * slice count they take and 16, 32 or 64 tasks per wave: the fastest is kept
  * when it beats the settings so far (its tasks per wave and slices are
  * then the ones returned; read the phases with
  * cwlb_ctx_get_column_phases), otherwise phases stay off.  In that mode

@@ -3,22 +3,26 @@
 With column phases (cwlb_ctx_set_column_phases, csrc/col_phases.hip and
 the PH branch of csrc/spmm_mean.hip) a task list that is a chain -- every
 task well formed and starting where its predecessor ended -- is executed
-P times.  Phase p gathers only the nonzeros of each row between the row's
-bounds B_p and B_{p+1}, where B_p(r) = row_ptr[r] + #{j in row r :
-floor(col[j] * P / h_rows) < p}.  A run of M tasks takes, whole, every row
-whose first nonzero lies in its tasks (the chain's first and last task keep
-their offsets), so each row has one owner: it is stored in the first phase
-and added to in the others.  Rows the chain covers only in part (its ends)
-are added to in every phase, after the clearing pass of the one-pass
-kernel.
+P times.  The bands interleave the columns: band(c) = c mod P.  Each call
+first writes a copy of the column and value arrays with every row's
+nonzeros stably sorted by band, and the bounds B_p(r) = row_ptr[r] +
+#{j in row r : band(col[j]) < p}; phase p gathers the copy's range
+[B_p(r), B_{p+1}(r)) of each row.  A run of M tasks takes, whole, every row
+whose first nonzero lies in its tasks, so each row has one owner: it is
+stored in the first phase and added to in the others.  Task offsets index
+the caller's order of a row's nonzeros, so the rows the chain covers only
+in part (its first row when it starts inside it, its last when it ends at
+an offset) are summed whole from the caller's arrays in the first phase,
+with the one-pass rules (after the one-pass clearing pass).
 
 This file restates those rules in Python and checks, against the oracle
 (the reference's task-at-a-time semantics, src/parallelMatrix.cpp:148-236):
 the partition's lists at many run lengths and phase counts, chains that
 start and end inside rows, unsorted rows and columns outside the feature
-matrix.  The bounds are checked against what they mean (every nonzero of
-phase p's range lies in band p when the row is sorted), and planted
-mistakes in the restated rules make the comparison fail.
+matrix.  The band sort is checked against what it means (the copy is a
+per-row permutation of the row's nonzeros, band p of a row is exactly its
+band-p nonzeros, in their original order), and planted mistakes in the
+restated rules make the comparison fail.
 """
 import numpy as np
 import pytest
@@ -36,8 +40,14 @@ def is_chain(tasks, n_rows):
 
 
 def bands(ci, h_rows, P):
+    """band_of in col_phases.hip: c mod P, columns outside [0, h_rows) in band 0."""
     c = ci.astype(np.int64)
-    return np.where(c < 0, 0, np.where(c >= h_rows, P - 1, c * P // max(h_rows, 1)))
+    return np.where((c < 0) | (c >= h_rows), 0, c % P)
+
+
+def row_ok(rp, nnz):
+    p0, p1 = rp[:-1].astype(np.int64), rp[1:].astype(np.int64)
+    return (p0 >= 0) & (p1 >= p0) & (p1 <= nnz)
 
 
 def phase_bounds(rp, ci, h_rows, P):
@@ -45,18 +55,34 @@ def phase_bounds(rp, ci, h_rows, P):
     n, nnz = len(rp) - 1, len(ci)
     out = np.zeros((P - 1, n), np.int64)
     b = bands(ci, h_rows, P)
-    p0, p1 = rp[:-1].astype(np.int64), rp[1:].astype(np.int64)
-    ok = (p0 >= 0) & (p1 >= p0) & (p1 <= nnz)
-    s0, s1 = np.where(ok, p0, 0), np.where(ok, p1, 0)
+    ok = row_ok(rp, nnz)
+    p0 = rp[:-1].astype(np.int64)
+    s0, s1 = np.where(ok, p0, 0), np.where(ok, rp[1:].astype(np.int64), 0)
     for q in range(1, P):
         cs = np.concatenate([[0], np.cumsum(b < q)])
         out[q - 1] = np.where(ok, p0 + cs[s1] - cs[s0], 0)
     return out
 
 
-def run_segments(tasks, M):
-    """The (rs, re, fo, ln) of every run: rows whose first nonzero lies in
-    the run, the chain's ends keeping their offsets (spmm_mean.hip, PH)."""
+def band_copy(rp, ci, val, h_rows, P):
+    """The band-sorted copy: each well-formed row's nonzeros stably sorted
+    by band (rows with bad offsets are not copied: left as `fill`)."""
+    ci_b, val_b = np.zeros_like(ci), np.zeros_like(val)
+    b = bands(ci, h_rows, P)
+    ok = row_ok(rp, len(ci))
+    for r in np.nonzero(ok)[0]:
+        p0, p1 = int(rp[r]), int(rp[r + 1])
+        order = np.argsort(b[p0:p1], kind="stable")
+        ci_b[p0:p1] = ci[p0:p1][order]
+        val_b[p0:p1] = val[p0:p1][order]
+    return ci_b, val_b
+
+
+def run_pieces(tasks, M):
+    """The pieces every run executes (spmm_mean.hip, PH branch): (rs, re,
+    fo, ln, banded) -- the whole rows whose first nonzero lies in the run,
+    band by band; the chain's partial first and last rows at the task
+    offsets, from the caller's arrays, in the first phase only."""
     T = len(tasks)
     zl = tasks[T - 1]
     out = []
@@ -65,28 +91,41 @@ def run_segments(tasks, M):
         z = tasks[min(t0 + M, T) - 1]
         head = t0 == 0
         rs = int(a[0]) if (head or a[2] == 0) else int(a[0]) + 1
+        re = int(z[1])
         fo = int(a[2]) if head else 0
         ln = int(zl[3]) if z[1] == zl[1] else 0
-        if rs < z[1]:
-            out.append((rs, int(z[1]), fo, ln))
+        if rs >= re:
+            continue
+        bs = rs + (1 if fo > 0 else 0)
+        be = max(bs, re - (1 if ln > 0 else 0))
+        if bs < be:
+            out.append((bs, be, 0, 0, True))
+        if fo > 0:
+            out.append((rs, rs + 1, fo, ln if (ln > 0 and re == rs + 1) else 0, False))
+        if ln > 0 and not (fo > 0 and re == rs + 1):
+            out.append((re - 1, re, 0, ln, False))
     return out
 
 
-def emulate_phased(rp, ci, val, origin, H, tasks, M, P, C0, rng, bounds=None,
-                   segments_of=run_segments, later_phase_adds=True):
+def emulate_phased(rp, ci, val, origin, H, tasks, M, P, C0, rng, copy=None,
+                   pieces_of=run_pieces, later_phase_adds=True):
     """C after the clearing pass and the P phase launches (float64)."""
     n_rows, nnz = len(rp) - 1, len(ci)
     C = C0.astype(np.float64)
     for o in cleared_rows(rp, origin, tasks, M, n_rows, nnz):
         C[o] = 0.0
-    B = phase_bounds(rp, ci, H.shape[0], P) if bounds is None else bounds
-    segs = segments_of(tasks, M)
+    B = phase_bounds(rp, ci, H.shape[0], P)
+    ci_b, val_b = band_copy(rp, ci, val, H.shape[0], P) if copy is None else copy
+    pieces = pieces_of(tasks, M)
     for p in range(P):
         first = p == 0
-        for k in rng.permutation(len(segs)):
-            seg = segs[k]
-            for r in range(max(seg[0], 0), min(seg[1], n_rows)):
-                base, b, e, d = row_chunk(rp, r, seg, nnz)
+        for k in rng.permutation(len(pieces)):
+            rs, re, fo, ln, banded = pieces[k]
+            if not banded and not first:
+                continue
+            cx, vx = (ci_b, val_b) if banded else (ci, val)
+            for r in range(max(rs, 0), min(re, n_rows)):
+                base, b, e, d = row_chunk(rp, r, (rs, re, fo, ln), nnz)
                 o = origin[r]
                 if d < 0:
                     continue
@@ -95,14 +134,13 @@ def emulate_phased(rp, ci, val, origin, H, tasks, M, P, C0, rng, bounds=None,
                         C[o] = 0.0
                     continue
                 own = b == 0 and e == d
-                lo = 0 if p == 0 else min(max(int(B[p - 1, r]) - base, 0), d)
-                hi = d if p == P - 1 else min(max(int(B[p, r]) - base, lo), d)
-                b, e = max(b, lo), max(min(e, hi), max(b, lo))
-                cols = ci[base + b:base + e]
-                acc = (val[base + b:base + e, None].astype(np.float64) * H[cols]).sum(0) / d
-                if own and first:
-                    C[o] = acc
-                elif own and not later_phase_adds:
+                if banded:
+                    lo = 0 if p == 0 else min(max(int(B[p - 1, r]) - base, 0), d)
+                    hi = d if p == P - 1 else min(max(int(B[p, r]) - base, lo), d)
+                    b, e = max(b, lo), max(min(e, hi), max(b, lo))
+                cols = cx[base + b:base + e]
+                acc = (vx[base + b:base + e, None].astype(np.float64) * H[cols]).sum(0) / d
+                if own and (first or not later_phase_adds):
                     C[o] = acc
                 elif e > b:
                     C[o] += acc
@@ -132,9 +170,9 @@ def test_partition_lists(cfg, S, P, M):
     phases give the reference's result with C not cleared beforehand."""
     p, H = small_problem(cfg, S, 2)
     assert is_chain(p.tasks, p.n)
-    segs = run_segments(p.tasks, M)
     owners = np.zeros(p.n, np.int64)
-    for rs, re, _, _ in segs:
+    for rs, re, _, _, banded in run_pieces(p.tasks, M):
+        assert banded  # the partition's chain starts and ends on row boundaries
         owners[rs:re] += 1
     assert (owners == 1).all()
     check(p, H, p.tasks, M, P, zero_output=False, rng=np.random.default_rng(P * M))
@@ -143,8 +181,9 @@ def test_partition_lists(cfg, S, P, M):
 @pytest.mark.parametrize("M", [1, 4, 64])
 def test_chains_that_start_and_end_inside_rows(M):
     """Sub-lists of the partition's list start and end inside split rows:
-    the chain's first and last rows are partial and added to; rows outside
-    keep C's contents (the reference's zeroed C here)."""
+    the chain's first and last rows are partial, summed from the caller's
+    arrays and added to; rows outside keep C's contents (the reference's
+    zeroed C here)."""
     rng = np.random.default_rng(M)
     p, H = small_problem(4, 3, 5)
     split = np.nonzero(p.tasks[:, 2] > 0)[0]
@@ -153,41 +192,50 @@ def test_chains_that_start_and_end_inside_rows(M):
         k, j = np.sort(rng.choice(split, 2, replace=False))
         sub = p.tasks[k:j + 1]
         assert sub[0, 2] > 0
+        owners = np.zeros(p.n, np.int64)
+        for rs, re, _, _, _ in run_pieces(sub, M):
+            owners[rs:re] += 1
+        assert owners.max() == 1
         check(p, H, sub, M, 4, zero_output=True, rng=rng)
+    # a chain inside one row
+    one = np.nonzero((p.tasks[:, 2] > 0) & (p.tasks[:, 3] > 0))[0]
+    sub = p.tasks[one[0]:one[0] + 1]
+    assert run_pieces(sub, 1) == [(int(sub[0, 0]), int(sub[0, 1]), int(sub[0, 2]),
+                                   int(sub[0, 3]), False)]
+    check(p, H, sub, 1, 3, zero_output=True, rng=rng)
 
 
-def test_bounds_split_rows_into_bands():
-    """Sorted rows: every nonzero of phase p's range has band p, the bounds
-    are non-decreasing and within the row; unsorted rows are still split
-    exactly (the phases partition each row)."""
+def test_band_sort_meaning():
+    """The copy is each row's nonzeros, stably sorted by band (c mod P):
+    the copy's range [B_p, B_{p+1}) of a row holds exactly the row's band-p
+    nonzeros, in their original order; columns outside [0, h_rows) are in
+    band 0; rows with bad offsets get bounds 0."""
     rng = np.random.default_rng(0)
     n, h = 300, 1000
     deg = rng.integers(0, 40, n)
     rp = np.concatenate([[0], np.cumsum(deg)]).astype(np.int64)
-    ci = rng.integers(0, h, rp[-1])
-    ci_sorted = ci.copy()
-    for r in range(n):
-        ci_sorted[rp[r]:rp[r + 1]].sort()
+    ci = rng.integers(-2, h + 3, rp[-1])
+    val = rng.normal(size=rp[-1]).astype(np.float32)
     for P in (2, 7, 64):
-        B = phase_bounds(rp, ci_sorted, h, P)
+        B = phase_bounds(rp, ci, h, P)
         full = np.concatenate([rp[None, :-1], B, rp[None, 1:]])
         assert (np.diff(full, axis=0) >= 0).all()
-        bnd = bands(ci_sorted, h, P)
-        for q in range(P):
-            for r in range(0, n, 17):
-                assert (bnd[full[q, r]:full[q + 1, r]] == q).all()
-        # unsorted: the counts per phase are still the band sizes
-        Bu = phase_bounds(rp, ci, h, P)
-        fu = np.concatenate([rp[None, :-1], Bu, rp[None, 1:]])
-        bu = bands(ci, h, P)
-        for r in range(0, n, 13):
+        ci_b, val_b = band_copy(rp, ci, val, h, P)
+        for r in range(0, n, 7):
+            row = slice(rp[r], rp[r + 1])
+            c, v = ci[row], val[row]
+            b = np.where((c < 0) | (c >= h), 0, c % P)
             for q in range(P):
-                assert fu[q + 1, r] - fu[q, r] == (bu[rp[r]:rp[r + 1]] == q).sum()
+                got_c = ci_b[full[q, r]:full[q + 1, r]]
+                got_v = val_b[full[q, r]:full[q + 1, r]]
+                assert np.array_equal(got_c, c[b == q]) and np.array_equal(got_v, v[b == q])
+    bad = rp.copy()
+    bad[10] = bad[11] + 3
+    assert (phase_bounds(bad, ci, h, 5)[:, 10] == 0).all()
 
 
-def test_unsorted_rows_and_foreign_bounds():
-    """Unsorted rows and bounds built for other contents of col_idx only
-    move nonzeros between phases: the result is the reference's."""
+def test_unsorted_rows():
+    """Rows whose columns are in any order: the result is the reference's."""
     rng = np.random.default_rng(3)
     p, H = small_problem(3, 6, 4)
     ci = p.col_idx.copy()
@@ -196,16 +244,16 @@ def test_unsorted_rows_and_foreign_bounds():
         rng.shuffle(seg)
     p.col_idx = ci
     check(p, H, p.tasks, 16, 6, zero_output=False, rng=rng)
-    other = rng.integers(0, p.n, len(ci)).astype(np.int32)
-    check(p, H, p.tasks, 16, 6, zero_output=False, rng=rng,
-          bounds=phase_bounds(p.row_ptr, other, p.n, 6))
 
 
 def test_planted_mistakes_fail():
     """Each plausible mistake in the run rule or the phase writes breaks
     the comparison: no +1 for a run that starts inside a row begun
-    earlier, the chain's last offset or first offset dropped, a later
-    phase storing instead of adding."""
+    earlier, the chain's last or first offset dropped, the partial rows
+    read from the band-sorted copy at the caller's offsets, a later phase
+    storing instead of adding.  (A copy left unsorted is no mistake of the
+    result: the bounds still split each row into P ranges that cover it
+    once; test_band_sort_meaning pins the sort.)"""
     rng = np.random.default_rng(7)
     p, H = small_problem(4, 3, 5)
     split = np.nonzero(p.tasks[:, 2] > 0)[0]
@@ -224,23 +272,29 @@ def test_planted_mistakes_fail():
     assert np.isfinite(ref).all()
 
     def no_plus_one(tasks, M):
-        segs = []
+        out = []
         for t0 in range(0, len(tasks), M):
             a, z = tasks[t0], tasks[min(t0 + M, len(tasks)) - 1]
-            segs.append((int(a[0]), int(z[1]), int(a[2]) if t0 == 0 else 0,
-                         int(tasks[-1][3]) if z[1] == tasks[-1][1] else 0))
-        return segs
+            out.append((int(a[0]), int(z[1]), int(a[2]) if t0 == 0 else 0,
+                        int(tasks[-1][3]) if z[1] == tasks[-1][1] else 0, False))
+        return out
 
     def no_tail(tasks, M):
-        return [(rs, re, fo, 0) for rs, re, fo, _ in run_segments(tasks, M)]
+        return [x if x[4] or x[3] == 0 else x[:3] + (0, False) for x in run_pieces(tasks, M)]
 
     def no_head(tasks, M):
-        return [(rs, re, 0, ln) for rs, re, _, ln in run_segments(tasks, M)]
+        return [x if x[4] or x[2] == 0 else (x[0], x[1], 0, x[3], False)
+                for x in run_pieces(tasks, M)]
 
-    assert differs(sub, segments_of=no_plus_one)
-    assert differs(sub, segments_of=no_tail)
-    assert differs(sub, segments_of=no_head)
+    def partial_from_copy(tasks, M):
+        return [x[:4] + (True,) for x in run_pieces(tasks, M)]
+
+    assert differs(sub, pieces_of=no_plus_one)
+    assert differs(sub, pieces_of=no_tail)
+    assert differs(sub, pieces_of=no_head)
+    assert differs(sub, pieces_of=partial_from_copy)
     assert differs(sub, later_phase_adds=False)
+    assert not differs(sub, copy=(p.col_idx, p.val))
 
 
 def test_broken_lists_are_not_chains():

@@ -1,14 +1,14 @@
 """GPU parity of the column-phased aggregation (cwlb_ctx_set_column_phases).
 
 The phased path runs a chain of tasks P times, phase p gathering the
-nonzeros whose column lies in band p of the feature matrix, each row owned
-by one wave (stored in the first phase, added to in the others).  Its
-results must be the reference's (the oracle, src/parallelMatrix.cpp:
-148-236) within the parity tolerance |gpu - ref| <= 1e-6 + 1e-5 |ref|, for
-every run length, slice count and phase count, for chains that start and
-end inside rows, and lists that are not chains must run in one pass with
-the one-pass results.  The device-built bounds must equal their host
-restatement exactly.
+nonzeros whose column c has c mod P = p from a band-sorted copy of the
+column and value arrays, each row owned by one wave (stored in the first
+phase, added to in the others).  Its results must be the reference's (the
+oracle, src/parallelMatrix.cpp:148-236) within the parity tolerance
+|gpu - ref| <= 1e-6 + 1e-5 |ref|, for every run length, slice count and
+phase count, for chains that start and end inside rows, and lists that are
+not chains must run in one pass with the one-pass results.  The device's
+band sort (bounds and copy) must equal its host restatement exactly.
 """
 import numpy as np
 import pytest
@@ -16,7 +16,7 @@ import pytest
 import oracle
 from conftest import SKEWED_COSTS, UNIT_COSTS
 from cwlb_amd import capi, synth, workloads
-from test_column_phases import phase_bounds
+from test_column_phases import band_copy, phase_bounds
 from test_gpu_spmm import check, custom_graph, dev, oracle_pair, problem, run_gpu, torch_mod
 
 pytestmark = pytest.mark.gpu
@@ -44,21 +44,26 @@ def expected_phases(K, SL, P):
     return P if -(-(K // 4) // sl) <= 64 else 1
 
 
-def device_bounds(ctx, rp, ci, h_rows, P):
+def device_band_sort(ctx, rp, ci, val, h_rows, P):
+    """(bounds, col copy, val copy) from cwlb_column_phase_bounds."""
     torch = torch_mod()
-    n = len(rp) - 1
+    n, nnz = len(rp) - 1, len(ci)
     out = torch.full(((P - 1) * max(n, 1),), -7, dtype=torch.int32, device="cuda")
-    ctx.column_phase_bounds(dev(rp), dev(ci), n, len(ci), h_rows, P, out)
+    col = torch.full((max(nnz, 1),), -9, dtype=torch.int32, device="cuda")
+    vals = torch.full((max(nnz, 1),), -9.0, dtype=torch.float32, device="cuda")
+    ctx.column_phase_bounds(dev(rp), dev(ci), dev(val), n, nnz, h_rows, P, out, col, vals)
     torch.cuda.synchronize()
-    return out.cpu().numpy()[:(P - 1) * n].reshape(P - 1, n)
+    return (out.cpu().numpy()[:(P - 1) * n].reshape(P - 1, n), col.cpu().numpy()[:nnz],
+            vals.cpu().numpy()[:nnz])
 
 
 @pytest.mark.parametrize("P", [2, 3, 16, 64])
-def test_bounds_match_host(gpu_ctx, P):
+def test_band_sort_matches_host(gpu_ctx, P):
     """Sorted and unsorted rows, columns below 0 and at or past h_rows, a
-    row of 3000 nonzeros (many 64-wide steps), empty rows and rows whose
-    offsets leave [0, nnz] or decrease: the device bounds equal the host
-    restatement exactly."""
+    row of 3000 nonzeros (many 64-wide steps) and empty rows: the device
+    bounds and band-sorted copy equal the host restatement exactly (the
+    copy is stable within each band).  Rows whose offsets leave [0, nnz] or
+    decrease get bounds 0."""
     rng = np.random.default_rng(P)
     n, h = 2000, 777
     deg = rng.integers(0, 90, n)
@@ -66,27 +71,40 @@ def test_bounds_match_host(gpu_ctx, P):
     deg[rng.integers(0, n, 200)] = 0
     rp = np.concatenate([[0], np.cumsum(deg)]).astype(np.int32)
     ci = rng.integers(-3, h + 4, rp[-1]).astype(np.int32)
+    val = rng.normal(size=rp[-1]).astype(np.float32)
     for r in range(0, n, 2):
         ci[rp[r]:rp[r + 1]].sort()
-    got = device_bounds(gpu_ctx, rp, ci, h, P)
-    assert np.array_equal(got, phase_bounds(rp, ci, h, P))
+    bounds, col, vals = device_band_sort(gpu_ctx, rp, ci, val, h, P)
+    assert np.array_equal(bounds, phase_bounds(rp, ci, h, P))
+    want_c, want_v = band_copy(rp, ci, val, h, P)
+    assert np.array_equal(col, want_c) and np.array_equal(vals, want_v)
     bad = rp.copy()
     bad[100] = bad[101] + 5       # row 100 decreases
     bad[-1] = rp[-1] + 50         # the last row passes nnz
-    got = device_bounds(gpu_ctx, bad, ci, h, P)
+    got, _, _ = device_band_sort(gpu_ctx, bad, ci, val, h, P)
     assert np.array_equal(got, phase_bounds(bad, ci, h, P))
     assert (got[:, 100] == 0).all() and (got[:, n - 1] == 0).all()
 
 
-def test_bounds_arguments(gpu_ctx):
+def test_band_sort_arguments(gpu_ctx):
     torch = torch_mod()
     rp, ci = dev(np.array([0, 1], np.int32)), dev(np.array([0], np.int32))
+    val = dev(np.array([1.0], np.float32))
     out = torch.zeros(64, dtype=torch.int32, device="cuda")
+    col = torch.zeros(64, dtype=torch.int32, device="cuda")
+    vals = torch.zeros(64, dtype=torch.float32, device="cuda")
     for P, h in ((1, 1), (65, 1), (2, 0)):
         with pytest.raises(capi.CwlbError) as e:
-            gpu_ctx.column_phase_bounds(rp, ci, 1, 1, h, P, out)
+            gpu_ctx.column_phase_bounds(rp, ci, val, 1, 1, h, P, out)
         assert e.value.status == capi.INVALID_ARG
-    gpu_ctx.column_phase_bounds(rp, ci, 0, 0, 1, 2, out)  # nothing to do
+    with pytest.raises(capi.CwlbError) as e:  # the two copies go together
+        gpu_ctx.column_phase_bounds(rp, ci, val, 1, 1, 1, 2, out, col, None)
+    assert e.value.status == capi.INVALID_ARG
+    with pytest.raises(capi.CwlbError) as e:  # a copy needs the values
+        gpu_ctx.column_phase_bounds(rp, ci, None, 1, 1, 1, 2, out, col, vals)
+    assert e.value.status == capi.INVALID_ARG
+    gpu_ctx.column_phase_bounds(rp, ci, val, 0, 0, 1, 2, out)  # nothing to do
+    gpu_ctx.column_phase_bounds(rp, ci, None, 1, 1, 1, 2, out)  # bounds only
 
 
 # (P, tasks per wave, slices)
@@ -227,8 +245,8 @@ def test_hub_row_degree_zero_rows_and_zero_output(gpu_ctx, reset, rng):
 
 
 def test_rewritten_columns_keep_results_right(gpu_ctx, reset):
-    """Bounds built for earlier contents of col_idx (same pointer, sizes and
-    P, so they are reused) only move nonzeros between phases."""
+    """Columns rewritten in place between two phased calls (same pointer and
+    sizes): every call sorts the arrays as they are."""
     torch = torch_mod()
     g = workloads.small(2, seed=4)
     K = 64
@@ -275,12 +293,14 @@ def test_bad_entries_are_reported(gpu_ctx, reset, bad):
     check(got, oracle.spmm_mean_f32(p.row_ptr, p.col_idx, p.val, p.origin, H, p.tasks))
 
 
-@pytest.mark.parametrize("built", [True, False], ids=["bounds_built", "bounds_unbuilt"])
-def test_graph_capture_and_replay(gpu_ctx, reset, built):
-    """A phased call captured into a HIP graph after an eager call built its
-    bounds replays the phases; without built bounds the captured call runs
-    in one pass.  Every replay, between eager work, gives the eager
-    result."""
+@pytest.mark.parametrize("built", [True, False], ids=["buffers_sized", "buffers_small"])
+def test_graph_capture_and_replay(gpu_ctx, built):
+    """A phased call captured into a HIP graph after an eager call sized the
+    context's phase buffers replays the band sort and the phases; with
+    buffers too small for its phase count the captured call runs in one
+    pass.  Every replay, between eager phased calls that rewrite the same
+    buffers, gives the eager result.  (A context of its own: the buffers'
+    sizes are the point.)"""
     torch = torch_mod()
     g = workloads.small(4, seed=21)
     K = 64
@@ -289,35 +309,40 @@ def test_graph_capture_and_replay(gpu_ctx, reset, built):
     d_t = dev(np.ascontiguousarray(p.tasks, np.int32).reshape(-1))
     H = dev(synth.features(g.n, K, 4))
     C = torch.zeros((g.n, K), dtype=torch.float32, device="cuda")
-    set_phased(gpu_ctx, 6 if built else 5, 8, 2)
-    if built:
-        gpu_ctx.spmm(d_rp, d_ci, d_v, d_o, g.n, g.nnz, H, g.n, K, d_t, len(p.tasks), C)
-    else:
-        # bounds for another phase count: not reusable under capture
-        gpu_ctx.set_column_phases(9)
-        gpu_ctx.spmm(d_rp, d_ci, d_v, d_o, g.n, g.nnz, H, g.n, K, d_t, len(p.tasks), C)
-        gpu_ctx.set_column_phases(5)
-    eager = C.clone()
-    graph = torch.cuda.CUDAGraph()
-    side = torch.cuda.Stream()
-    side.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(side):
-        gpu_ctx.set_stream(side.cuda_stream)
-        with torch.cuda.graph(graph, stream=side):
-            gpu_ctx.spmm(d_rp, d_ci, d_v, d_o, g.n, g.nnz, H, g.n, K, d_t, len(p.tasks), C,
+    ctx = capi.Context(0, torch.cuda.current_stream().cuda_stream)
+    try:
+        # The phased calls of the test have 6 phases; the buffers come from
+        # an eager call with 6 phases, or with 3 (2 bounds per row: too
+        # small for 6 phases under capture).
+        set_phased(ctx, 6 if built else 3, 8, 2)
+        ctx.spmm(d_rp, d_ci, d_v, d_o, g.n, g.nnz, H, g.n, K, d_t, len(p.tasks), C)
+        ctx.set_column_phases(6)
+        eager = C.clone()
+        graph = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            ctx.set_stream(side.cuda_stream)
+            with torch.cuda.graph(graph, stream=side):
+                ctx.spmm(d_rp, d_ci, d_v, d_o, g.n, g.nnz, H, g.n, K, d_t, len(p.tasks), C,
                          timed=False)
-    gpu_ctx.set_stream(torch.cuda.current_stream().cuda_stream)
-    assert gpu_ctx.last_launch()["column_phases"] == (6 if built else 1)
-    torch.cuda.synchronize()
-    for i in range(4):
-        C.fill_(float(i))
+        ctx.set_stream(torch.cuda.current_stream().cuda_stream)
+        assert ctx.last_launch()["column_phases"] == (6 if built else 1)
         torch.cuda.synchronize()
-        graph.replay()
-        torch.cuda.synchronize()
-        np.testing.assert_allclose(C.cpu().numpy(), eager.cpu().numpy(), rtol=1e-5, atol=1e-6)
-        # eager phased calls on another list between replays
-        gpu_ctx.spmm(d_rp, d_ci, d_v, d_o, g.n, g.nnz, H, g.n, K, d_t, len(p.tasks) // 2,
+        for i in range(4):
+            C.fill_(float(i))
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            np.testing.assert_allclose(C.cpu().numpy(), eager.cpu().numpy(), rtol=1e-5,
+                                       atol=1e-6)
+            # eager phased calls on another list between replays
+            ctx.spmm(d_rp, d_ci, d_v, d_o, g.n, g.nnz, H, g.n, K, d_t, len(p.tasks) // 2,
                      torch.zeros_like(C))
+        torch.cuda.synchronize()
+        del graph
+    finally:
+        ctx.close()
     ref32 = oracle.spmm_mean_f32(p.row_ptr, p.col_idx, p.val, p.origin, H.cpu().numpy(), p.tasks)
     np.testing.assert_allclose(C.cpu().numpy(), ref32, rtol=1e-5, atol=1e-6)
 
