@@ -430,26 +430,26 @@ cwlb_status cwlb_ctx_get_column_phases(cwlb_ctx* ctx, int32_t* phases)
     return CWLB_OK;
 }
 
-cwlb_status cwlb_column_phase_bounds(cwlb_ctx* ctx, const int32_t* row_ptr,
-                                     const int32_t* col_idx, const float* val, int32_t n_rows,
-                                     int64_t nnz, int64_t h_rows, int32_t phases,
-                                     int32_t* bounds_out, int32_t* col_out, float* val_out)
+cwlb_status cwlb_column_phase_sort(cwlb_ctx* ctx, const int32_t* row_ptr,
+                                   const int32_t* col_idx, const float* val, int32_t n_rows,
+                                   int64_t nnz, int64_t h_rows, int32_t phases,
+                                   int32_t* bounds_out, int32_t* col_out, float* val_out)
 {
     if (!ctx) return fail(CWLB_INVALID_ARG, "null context");
     if (phases < 2 || phases > 64)
-        return fail(CWLB_INVALID_ARG, "cwlb_column_phase_bounds: phases must be in [2, 64]");
+        return fail(CWLB_INVALID_ARG, "cwlb_column_phase_sort: phases must be in [2, 64]");
     if (n_rows < 0 || nnz < 0 || nnz > INT32_MAX || h_rows <= 0)
-        return fail(CWLB_INVALID_ARG, "cwlb_column_phase_bounds: n_rows >= 0, 0 <= nnz < 2^31 "
+        return fail(CWLB_INVALID_ARG, "cwlb_column_phase_sort: n_rows >= 0, 0 <= nnz < 2^31 "
                                       "and h_rows > 0 required");
     if (!col_out != !val_out)
         return fail(CWLB_INVALID_ARG,
-                    "cwlb_column_phase_bounds: col_out and val_out go together");
+                    "cwlb_column_phase_sort: col_out and val_out go together");
     if (n_rows > 0 && (!row_ptr || (nnz > 0 && (!col_idx || (col_out && !val)))))
-        return fail(CWLB_INVALID_ARG, "cwlb_column_phase_bounds: null array");
+        return fail(CWLB_INVALID_ARG, "cwlb_column_phase_sort: null array");
     DeviceGuard g(ctx->device);
     (void)hipGetLastError();
-    return launch_phase_bounds(ctx->stream, row_ptr, col_idx, val, n_rows, nnz, h_rows, phases,
-                               bounds_out, col_out, val_out);
+    return launch_band_sort(ctx->stream, row_ptr, col_idx, val, n_rows, nnz, h_rows, phases,
+                            bounds_out, col_out, val_out);
 }
 
 cwlb_status cwlb_ctx_last_launch(cwlb_ctx* ctx, cwlb_launch_info* out)

@@ -202,9 +202,9 @@ cwlb_status grow(cwlb_ctx* ctx, T** p, long long* cap, long long want)
 
 }  // namespace
 
-cwlb_status launch_phase_bounds(hipStream_t st, const int32_t* row_ptr, const int32_t* col_idx,
-                                const float* val, int32_t n_rows, int64_t nnz, int64_t h_rows,
-                                int phases, int32_t* bounds, int32_t* col_out, float* val_out)
+cwlb_status launch_band_sort(hipStream_t st, const int32_t* row_ptr, const int32_t* col_idx,
+                             const float* val, int32_t n_rows, int64_t nnz, int64_t h_rows,
+                             int phases, int32_t* bounds, int32_t* col_out, float* val_out)
 {
     if (n_rows <= 0 || phases < 2) return CWLB_OK;
     hipLaunchKernelGGL(band_sort, dim3(band_grid(n_rows)), dim3(kBlock), 0, st, row_ptr, col_idx,

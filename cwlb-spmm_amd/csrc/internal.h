@@ -188,9 +188,9 @@ cwlb_status prepare_column_phases(cwlb_ctx* ctx, const SpmmArgs& a, int phases, 
 // Enqueues the band sort: bounds[(p - 1) * n_rows + r] for p in [1, phases)
 // (bounds may be null) and, when col_out is non-null, the band-sorted copy
 // of col_idx and val.
-cwlb_status launch_phase_bounds(hipStream_t st, const int32_t* row_ptr, const int32_t* col_idx,
-                                const float* val, int32_t n_rows, int64_t nnz, int64_t h_rows,
-                                int phases, int32_t* bounds, int32_t* col_out, float* val_out);
+cwlb_status launch_band_sort(hipStream_t st, const int32_t* row_ptr, const int32_t* col_idx,
+                             const float* val, int32_t n_rows, int64_t nnz, int64_t h_rows,
+                             int phases, int32_t* bounds, int32_t* col_out, float* val_out);
 
 cwlb_status launch_reorder(cwlb_ctx* ctx, int32_t n_rows, int64_t nnz, const int32_t* row_ptr,
                            const int32_t* col_idx, const float* val, int32_t* origin,

@@ -1254,8 +1254,8 @@ cwlb_status launch_spmm_mean(cwlb_ctx* ctx, const SpmmArgs& a, bool zero_all, bo
     // copy, and always runs the clearing pass: it also checks the chain.
     if (p.phases > 1) {
         const cwlb_status s =
-            launch_phase_bounds(st, a.row_ptr, a.col_idx, a.val, a.n_rows, a.nnz, a.h_rows,
-                                p.phases, ph_arr.bounds, ph_arr.col, ph_arr.val);
+            launch_band_sort(st, a.row_ptr, a.col_idx, a.val, a.n_rows, a.nnz, a.h_rows,
+                             p.phases, ph_arr.bounds, ph_arr.col, ph_arr.val);
         if (s != CWLB_OK) return s;
     }
     if ((!zero_all || p.phases > 1) && work) {

@@ -25,7 +25,7 @@ EXPORTS = [
     "cwlb_ctx_set_stream", "cwlb_ctx_synchronize", "cwlb_ctx_device_info", "cwlb_ctx_set_schedule",
     "cwlb_ctx_set_locality", "cwlb_ctx_set_cache_hints", "cwlb_ctx_get_cache_hints",
     "cwlb_ctx_last_launch", "cwlb_ctx_set_occupancy", "cwlb_ctx_get_occupancy",
-    "cwlb_ctx_set_column_phases", "cwlb_ctx_get_column_phases", "cwlb_column_phase_bounds",
+    "cwlb_ctx_set_column_phases", "cwlb_ctx_get_column_phases", "cwlb_column_phase_sort",
     "cwlb_ctx_tune_schedule",
     "cwlb_spmm_mean_f32", "cwlb_spmm_mean_f32_large_k", "cwlb_spmm_mean_f32_host",
     "cwlb_spmm_mean_f32_noalloc",
@@ -126,7 +126,7 @@ def lib():
         L.cwlb_ctx_get_occupancy.argtypes = [vp, C.POINTER(i32)]
         L.cwlb_ctx_set_column_phases.argtypes = [vp, i32]
         L.cwlb_ctx_get_column_phases.argtypes = [vp, C.POINTER(i32)]
-        L.cwlb_column_phase_bounds.argtypes = [vp, vp, vp, vp, i32, i64, i64, i32, vp, vp, vp]
+        L.cwlb_column_phase_sort.argtypes = [vp, vp, vp, vp, i32, i64, i64, i32, vp, vp, vp]
         L.cwlb_ctx_tune_schedule.argtypes = [vp, vp, vp, vp, vp, i32, i64, vp, i64, i32, vp, i64,
                                              vp, i32, C.POINTER(i32), C.POINTER(i32), vp]
         spmm = [vp, vp, vp, vp, vp, i32, i64, vp, i64, i32, vp, i64, vp, u32, C.POINTER(Timing)]
@@ -339,10 +339,10 @@ class Context:
         check(lib().cwlb_ctx_get_column_phases(self.h, C.byref(v)))
         return v.value
 
-    def column_phase_bounds(self, row_ptr, col_idx, val, n_rows, nnz, h_rows, phases,
+    def column_phase_sort(self, row_ptr, col_idx, val, n_rows, nnz, h_rows, phases,
                             bounds_out=None, col_out=None, val_out=None):
-        """cwlb_column_phase_bounds on device tensors (enqueued on the stream)."""
-        check(lib().cwlb_column_phase_bounds(self.h, _ptr(row_ptr), _ptr(col_idx), _ptr(val),
+        """cwlb_column_phase_sort on device tensors (enqueued on the stream)."""
+        check(lib().cwlb_column_phase_sort(self.h, _ptr(row_ptr), _ptr(col_idx), _ptr(val),
                                              int(n_rows), int(nnz), int(h_rows), int(phases),
                                              _ptr(bounds_out), _ptr(col_out), _ptr(val_out)))
 

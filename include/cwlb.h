@@ -165,7 +165,7 @@ cwlb_status cwlb_ctx_get_occupancy(cwlb_ctx* ctx, int32_t* waves_per_simd);
  * communities numbered as ranges of ids spread over all passes).  Each
  * phased call first writes, into context-owned buffers, a copy of col_idx
  * and val with every row's nonzeros stably sorted by band and the row
- * bounds of the bands (see cwlb_column_phase_bounds; 8 bytes per nonzero
+ * bounds of the bands (see cwlb_column_phase_sort; 8 bytes per nonzero
  * and 4 (P - 1) per row, kept and grown as needed; about 0.3 ms on a
  * 115M-nonzero graph, reported in the timing's zero_us), so rewritten
  * arrays are always read as they are.  A row that one stretch of
@@ -201,10 +201,10 @@ cwlb_status cwlb_ctx_get_column_phases(cwlb_ctx* ctx, int32_t* phases);
  * row_ptr[r + 1].  A row whose offsets leave [0, nnz] or decrease gets
  * bounds 0 and is not copied.  No counterpart in the reference; the
  * column-phased aggregation runs this itself, tests read it here. */
-cwlb_status cwlb_column_phase_bounds(cwlb_ctx* ctx, const int32_t* row_ptr,
-                                     const int32_t* col_idx, const float* val, int32_t n_rows,
-                                     int64_t nnz, int64_t h_rows, int32_t phases,
-                                     int32_t* bounds_out, int32_t* col_out, float* val_out);
+cwlb_status cwlb_column_phase_sort(cwlb_ctx* ctx, const int32_t* row_ptr,
+                                   const int32_t* col_idx, const float* val, int32_t n_rows,
+                                   int64_t nnz, int64_t h_rows, int32_t phases,
+                                   int32_t* bounds_out, int32_t* col_out, float* val_out);
 
 /* The schedule the last aggregation launch on this context used, as the
  * automatic choices and the context's settings resolved it (all zero before

@@ -51,7 +51,7 @@ def row_ok(rp, nnz):
 
 
 def phase_bounds(rp, ci, h_rows, P):
-    """cwlb_column_phase_bounds: out[p - 1][r] = B_p(r), p in [1, P)."""
+    """cwlb_column_phase_sort: out[p - 1][r] = B_p(r), p in [1, P)."""
     n, nnz = len(rp) - 1, len(ci)
     out = np.zeros((P - 1, n), np.int64)
     b = bands(ci, h_rows, P)

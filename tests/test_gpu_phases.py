@@ -45,13 +45,13 @@ def expected_phases(K, SL, P):
 
 
 def device_band_sort(ctx, rp, ci, val, h_rows, P):
-    """(bounds, col copy, val copy) from cwlb_column_phase_bounds."""
+    """(bounds, col copy, val copy) from cwlb_column_phase_sort."""
     torch = torch_mod()
     n, nnz = len(rp) - 1, len(ci)
     out = torch.full(((P - 1) * max(n, 1),), -7, dtype=torch.int32, device="cuda")
     col = torch.full((max(nnz, 1),), -9, dtype=torch.int32, device="cuda")
     vals = torch.full((max(nnz, 1),), -9.0, dtype=torch.float32, device="cuda")
-    ctx.column_phase_bounds(dev(rp), dev(ci), dev(val), n, nnz, h_rows, P, out, col, vals)
+    ctx.column_phase_sort(dev(rp), dev(ci), dev(val), n, nnz, h_rows, P, out, col, vals)
     torch.cuda.synchronize()
     return (out.cpu().numpy()[:(P - 1) * n].reshape(P - 1, n), col.cpu().numpy()[:nnz],
             vals.cpu().numpy()[:nnz])
@@ -95,16 +95,16 @@ def test_band_sort_arguments(gpu_ctx):
     vals = torch.zeros(64, dtype=torch.float32, device="cuda")
     for P, h in ((1, 1), (65, 1), (2, 0)):
         with pytest.raises(capi.CwlbError) as e:
-            gpu_ctx.column_phase_bounds(rp, ci, val, 1, 1, h, P, out)
+            gpu_ctx.column_phase_sort(rp, ci, val, 1, 1, h, P, out)
         assert e.value.status == capi.INVALID_ARG
     with pytest.raises(capi.CwlbError) as e:  # the two copies go together
-        gpu_ctx.column_phase_bounds(rp, ci, val, 1, 1, 1, 2, out, col, None)
+        gpu_ctx.column_phase_sort(rp, ci, val, 1, 1, 1, 2, out, col, None)
     assert e.value.status == capi.INVALID_ARG
     with pytest.raises(capi.CwlbError) as e:  # a copy needs the values
-        gpu_ctx.column_phase_bounds(rp, ci, None, 1, 1, 1, 2, out, col, vals)
+        gpu_ctx.column_phase_sort(rp, ci, None, 1, 1, 1, 2, out, col, vals)
     assert e.value.status == capi.INVALID_ARG
-    gpu_ctx.column_phase_bounds(rp, ci, val, 0, 0, 1, 2, out)  # nothing to do
-    gpu_ctx.column_phase_bounds(rp, ci, None, 1, 1, 1, 2, out)  # bounds only
+    gpu_ctx.column_phase_sort(rp, ci, val, 0, 0, 1, 2, out)  # nothing to do
+    gpu_ctx.column_phase_sort(rp, ci, None, 1, 1, 1, 2, out)  # bounds only
 
 
 # (P, tasks per wave, slices)
