@@ -35,6 +35,11 @@
 //   * the occupancy variant (O6) keeps UL <= 2, which lets slots of 4 to 16
 //     lanes fit 80 VGPRs: 6 waves per SIMD instead of 5, for graphs of
 //     short rows, where waves in flight set the speed;
+//   * column phases (PH, csrc/col_phases.hip): the launch is repeated once
+//     per band of columns (c mod P) over a copy of the CSR sorted by band
+//     within each row, so that the feature rows all waves gather at a time
+//     fit the caches; on a chain of tasks each run owns whole rows, stored
+//     in the first phase and added to without atomics in the others;
 //   * column indices and values are fetched with coalesced streaming loads:
 //     64 at a time for a long chunk, handed to the slots with cross-lane
 //     shuffles; for a group of short rows, the group's whole contiguous
