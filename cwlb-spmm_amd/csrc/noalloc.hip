@@ -83,8 +83,9 @@ extern "C" cwlb_status cwlb_spmm_mean_f32_noalloc(
     DeviceSlot& slot = g_slots[device];
     std::call_once(slot.once, [&] { init_slot(slot, device); });
     if (slot.st != CWLB_OK) return fail(slot.st, slot.err);
-    if (tasks_per_wave < 0)
-        return fail(CWLB_INVALID_ARG, "tasks_per_wave must be >= 0 (0 = automatic)");
+    if (tasks_per_wave < 0 || tasks_per_wave > (1 << 20))
+        return fail(CWLB_INVALID_ARG,
+                    "tasks_per_wave must be in [0, 1048576] (0 = automatic)");
     if (feature_slices != 0 && feature_slices != 1 && feature_slices != 2 &&
         feature_slices != 4 && feature_slices != 8)
         return fail(CWLB_INVALID_ARG, "feature_slices must be 0, 1, 2, 4 or 8");

@@ -89,7 +89,7 @@ def test_noalloc_large_k_and_errors(gpu_ctx):
     capi.spmm_noalloc(stream, d[0], d[1], d[2], d[3], g.n, g.nnz, d_H, g.n, 1100, d_t,
                       len(p.tasks), C)
     np.testing.assert_allclose(C.cpu().numpy(), want, rtol=RTOL, atol=ATOL)
-    for kw in ({"tasks_per_wave": -1}, {"feature_slices": 3}):
+    for kw in ({"tasks_per_wave": -1}, {"tasks_per_wave": (1 << 20) + 1}, {"feature_slices": 3}):
         with pytest.raises(capi.CwlbError) as e:
             capi.spmm_noalloc(stream, d[0], d[1], d[2], d[3], g.n, g.nnz, d_H, g.n, 1100, d_t,
                               len(p.tasks), C, **kw)
