@@ -359,7 +359,7 @@ cwlb_status cwlb_spmm_mean_f32_host(cwlb_ctx* ctx, const int32_t* row_ptr,
  * needs no context: it runs on the current HIP device and the given stream
  * (NULL = the null stream), with the automatic schedule or the given tasks
  * per wave and feature slices (as cwlb_ctx_set_schedule; 0 = automatic), in
- * task order and without cache hints.  Any K is accepted (both
+ * task order, in one pass (no column phases) and without cache hints.  Any K is accepted (both
  * cwlb_spmm_mean_f32's range and the large-K entry's); flags and results
  * are those of cwlb_spmm_mean_f32.  It calls no hipMalloc, hipFree or other
  * allocating routine: the kernels' status word lives in a 256-byte device
