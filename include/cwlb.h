@@ -174,10 +174,10 @@ cwlb_status cwlb_ctx_get_occupancy(cwlb_ctx* ctx, int32_t* waves_per_simd);
  * writes C P times: phases pay when H is well beyond the 256 MB Infinity
  * Cache, the columns of a row are spread over H and rows hold many more
  * nonzeros than 2P (measured: a 240k-row block model with 480 nonzeros per
- * row and K = 600, 12 phases: 28.1 ms per call against 37.2 ms).  Under graph capture the
- * buffers are only used when an earlier call sized them (otherwise the
- * call runs in one pass); a buffer a capture used is never freed before
- * cwlb_ctx_destroy.  Applies to task lists that are chains -- every task
+ * row and K = 600, 12 phases: 27.6 ms per call against 37.2 ms).  Under
+ * graph capture the buffers are only used when an earlier call sized them
+ * (otherwise the call runs in one pass); a buffer a capture used is never
+ * freed before cwlb_ctx_destroy.  Applies to task lists that are chains -- every task
  * well formed and starting where its predecessor ended, as
  * cwlb_partition's lists are -- which the device checks on every call; any
  * other list runs in one pass (over the band-sorted copy).  Applies with
