@@ -322,13 +322,14 @@ def schedule_build_times(call_fresh, sched):
     """Wall time (ms) that the chosen schedule's one-off builds add to the
     first call on a new context: the cache hints (column in-degrees, their
     histogram, one bit per nonzero), the run order sorted by output row and
-    the column phases' row bounds.  Each is the first call's time minus the
-    second's, on a context that has only that setting."""
+    the column phases' buffers (their allocation: the band sort itself runs
+    in every call, inside the step).  Each is the first call's time minus
+    the second's, on a context that has only that setting."""
     out = {"cache_hint_build_ms": None, "run_order_build_ms": None,
-           "column_phase_build_ms": None}
+           "column_phase_alloc_ms": None}
     if sched.get("phases", 0) > 1:
         first, second = call_fresh({"phases": sched["phases"]})
-        out["column_phase_build_ms"] = round(first - second, 2)
+        out["column_phase_alloc_ms"] = round(first - second, 2)
     if sched["hot_bytes"] > 0:
         first, second = call_fresh({"hot_bytes": sched["hot_bytes"]})
         out["cache_hint_build_ms"] = round(first - second, 2)
@@ -547,7 +548,7 @@ def main():
     prep.update(schedule_build_times(call_fresh, schedule))
     log(f"schedule builds: hints {prep['cache_hint_build_ms']} ms, "
         f"run order {prep['run_order_build_ms']} ms, "
-        f"phase bounds {prep['column_phase_build_ms']} ms")
+        f"phase buffers {prep['column_phase_alloc_ms']} ms")
     # The reference's structure (one task per wave, one atomic add per
     # partial segment), for comparison.
     pt = [ctx.spmm(d_rp, d_ci, d_v, d_o, g.n, g.nnz, H, g.n, K, d_t, T, C,
