@@ -435,3 +435,25 @@ def test_stream_switch_after_builds(gpu_ctx, reset):
     assert (info["column_phases"], info["run_order"]) == (7, 2), info
     check(Ca.cpu().numpy(), ref)
     check(Cb.cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("P", [3, 16])
+def test_duplicate_and_unsorted_columns(gpu_ctx, reset, rng, P):
+    """Rows that repeat columns in any order, with non-unit values: the band
+    sort keeps every copy (stable within a band) and the phased result is
+    the reference's."""
+    n = 3000
+    deg = rng.integers(0, 60, n)
+    rp = np.concatenate([[0], np.cumsum(deg)]).astype(np.int32)
+    ci = rng.integers(0, 50, rp[-1]).astype(np.int32)  # many repeats per row
+    val = rng.normal(size=rp[-1]).astype(np.float32)
+    g = custom_graph(rp, ci, val)
+    H = synth.features(n, 64, 3)
+    for S in (2, 17):
+        p = problem(g, SKEWED_COSTS, S)
+        set_phased(gpu_ctx, P, 8, 2)
+        got, _ = run_gpu(gpu_ctx, p, H)
+        assert gpu_ctx.last_launch()["column_phases"] == P
+        ref32, ref64 = oracle_pair(p, g, H)
+        check(got, ref32)
+        check(got, ref64)
