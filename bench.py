@@ -187,7 +187,9 @@ def pmc_child(args):
     d = [dev(x) for x in (rp, ci, val, origin, tasks.reshape(-1))]
     H = torch.empty((g.n, K), dtype=torch.float32, device="cuda")
     ctx.fill_features(H, g.n, K, workloads.FEATURE_SEED)
-    C = torch.empty((g.n, K), dtype=torch.float32, device="cuda")
+    # Cleared once, as the reference clears its output: rows the partition
+    # leaves out (empty rows costlier than the capacity) stay 0.
+    C = torch.zeros((g.n, K), dtype=torch.float32, device="cuda")
     ctx.set_schedule(args.tasks_per_wave, args.slices)
     ctx.set_locality(args.run_order, args.xcd_blocks)
     ctx.set_cache_hints(args.hot_mb << 20)
@@ -422,7 +424,9 @@ def main():
     d_rp, d_ci, d_v, d_o = dev(rp), dev(ci), dev(val), dev(origin)
     H = torch.empty((g.n, K), dtype=torch.float32, device="cuda")
     ctx.fill_features(H, g.n, K, workloads.FEATURE_SEED)
-    C = torch.empty((g.n, K), dtype=torch.float32, device="cuda")
+    # Cleared once, as the reference clears its output: rows the partition
+    # leaves out (empty rows costlier than the capacity) stay 0.
+    C = torch.zeros((g.n, K), dtype=torch.float32, device="cuda")
 
     def tasks_for(S):
         cap = capi.capacity_from_s(S, costs)

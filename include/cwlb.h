@@ -250,8 +250,12 @@ cwlb_status cwlb_ctx_last_launch(cwlb_ctx* ctx, cwlb_launch_info* out);
  * list in which no two tasks share a nonzero -- in any order, with gaps --
  * gives the reference's result; lists whose tasks overlap need
  * CWLB_SPMM_PER_TASK as well.  Without the flag, rows whose first nonzero
- * no task covers keep their previous contents (a partition from
- * cwlb_partition covers every row).
+ * no task covers keep their previous contents.  A partition from
+ * cwlb_partition covers every row with nonzeros; it leaves out the rows
+ * without nonzeros when their slot cost Cs exceeds the capacity (as the
+ * reference's does, utils.cpp:972-976), and the reference's result for
+ * them is the 0 of its cleared C: clear C once (this flag on the first
+ * call) before calls without it.
  * K == 0 or n_tasks == 0: C is cleared (when CWLB_SPMM_ZERO_OUTPUT is set)
  * and timings are 0, as the reference returns a zero matrix with time 0
  * (parallelMatrix.cpp:80-83, 101-104).

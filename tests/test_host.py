@@ -80,6 +80,27 @@ def test_partition_special_values():
             assert np.array_equal(got, oracle.ref_partition(rp, costs, cap))
 
 
+def test_partition_leaves_out_empty_rows_above_capacity():
+    """A row without nonzeros whose slot cost Cs exceeds the capacity gets no
+    task (utils.cpp:972-976: nothing of it remains to split); with Cs within
+    the capacity it is packed like any row.  Degrees 0, 0, 3, 0, 5 at S = 2
+    (capacity 0.5 + 1 * 2 = 2.5), derived by hand from the packing rules."""
+    rp = np.array([0, 0, 0, 3, 3, 8], np.int32)
+    cases = [((0.5, 0.5, 4.0, 0.5),   # Cs = 4 > 2.5: rows 0, 1, 3 left out
+              [[2, 3, 0, 2], [2, 3, 2, 0], [4, 5, 0, 2], [4, 5, 2, 4], [4, 5, 4, 0]]),
+             ((0.5, 0.5, 1.0, 0.5),   # Cs = 1: rows 0 and 1 packed, row 3 leads row 4
+              [[0, 2, 0, 0], [2, 3, 0, 2], [2, 3, 2, 0], [3, 5, 0, 1], [4, 5, 1, 3],
+               [4, 5, 3, 0]])]
+    for costs, want in cases:
+        cap = capi.capacity_from_s(2, costs)
+        assert cap == 2.5
+        got = capi.partition(rp, costs, cap)
+        assert got.tolist() == want
+        assert np.array_equal(got, oracle.partition(rp, costs, cap))
+        if oracle.ref() is not None:
+            assert np.array_equal(got, oracle.ref_partition(rp, costs, cap))
+
+
 def test_partition_empty_and_buffer_sizing():
     assert len(capi.partition(np.zeros(1, np.int32), UNIT_COSTS, 4.5)) == 0
     import ctypes as C
