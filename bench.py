@@ -187,8 +187,11 @@ def pmc_child(args):
     d = [dev(x) for x in (rp, ci, val, origin, tasks.reshape(-1))]
     H = torch.empty((g.n, K), dtype=torch.float32, device="cuda")
     ctx.fill_features(H, g.n, K, workloads.FEATURE_SEED)
-    # Cleared once, as the reference clears its output: rows the partition
-    # leaves out (empty rows costlier than the capacity) stay 0.
+    # Cleared once before the steps, as the reference clears its output
+    # outside its timed kernel (parallelMatrix.cpp:112): the rows without
+    # nonzeros, which its kernel never writes (:166), stay 0 -- the steps
+    # leave them (KEEP_EMPTY_ROWS) -- and so do the rows the partition
+    # leaves out (empty rows costlier than the capacity).
     C = torch.zeros((g.n, K), dtype=torch.float32, device="cuda")
     ctx.set_schedule(args.tasks_per_wave, args.slices)
     ctx.set_locality(args.run_order, args.xcd_blocks)
@@ -197,7 +200,7 @@ def pmc_child(args):
     ctx.set_column_phases(args.phases)
     for _ in range(1 + args.steps):
         ctx.spmm(d[0], d[1], d[2], d[3], g.n, g.nnz, H, g.n, K, d[4], len(tasks), C,
-                 large_k=large_k)
+                 flags=capi.KEEP_EMPTY_ROWS, large_k=large_k)
     nb = args.copy_probe_mib << 20
     src = torch.ones(nb // 4, dtype=torch.float32, device="cuda")
     dst = torch.empty_like(src)
@@ -424,8 +427,11 @@ def main():
     d_rp, d_ci, d_v, d_o = dev(rp), dev(ci), dev(val), dev(origin)
     H = torch.empty((g.n, K), dtype=torch.float32, device="cuda")
     ctx.fill_features(H, g.n, K, workloads.FEATURE_SEED)
-    # Cleared once, as the reference clears its output: rows the partition
-    # leaves out (empty rows costlier than the capacity) stay 0.
+    # Cleared once before the steps, as the reference clears its output
+    # outside its timed kernel (parallelMatrix.cpp:112): the rows without
+    # nonzeros, which its kernel never writes (:166), stay 0 -- the steps
+    # leave them (KEEP_EMPTY_ROWS) -- and so do the rows the partition
+    # leaves out (empty rows costlier than the capacity).
     C = torch.zeros((g.n, K), dtype=torch.float32, device="cuda")
 
     def tasks_for(S):
@@ -434,7 +440,7 @@ def main():
 
     def call(d_t, n_t, timed, c=ctx):
         return c.spmm(d_rp, d_ci, d_v, d_o, g.n, g.nnz, H, g.n, K, d_t, n_t, C, timed=timed,
-                      large_k=large_k)
+                      flags=capi.KEEP_EMPTY_ROWS, large_k=large_k)
 
     def tune(d_t, n_t):
         return ctx.tune_schedule(d_rp, d_ci, d_v, d_o, g.n, g.nnz, H, g.n, K, d_t, n_t, C,
@@ -554,9 +560,10 @@ def main():
         f"run order {prep['run_order_build_ms']} ms, "
         f"phase buffers {prep['column_phase_alloc_ms']} ms")
     # The reference's structure (one task per wave, one atomic add per
-    # partial segment), for comparison.
+    # partial segment, rows without nonzeros left), for comparison.
     pt = [ctx.spmm(d_rp, d_ci, d_v, d_o, g.n, g.nnz, H, g.n, K, d_t, T, C,
-                   flags=capi.PER_TASK, large_k=large_k) for _ in range(10)]
+                   flags=capi.PER_TASK | capi.KEEP_EMPTY_ROWS, large_k=large_k)
+          for _ in range(10)]
     per_task_us = float(np.mean([t.total_us for t in pt]))
 
     # The host-pointer boundary (the drop-in spmmKernel's transfers): one
@@ -591,6 +598,7 @@ def main():
     flops = 2.0 * g.nnz * K
     gflops = flops / (ms_per_step * 1e-3) / 1e9
     b_alg = workloads.algorithmic_bytes(g.n, g.nnz, K, T)
+    n_empty = int(np.count_nonzero(np.diff(rp) == 0))
     referenced = int(np.count_nonzero(np.bincount(g.col_idx, minlength=g.n)))
     b_min = workloads.compulsory_bytes(referenced, g.n, g.nnz, K) + 16 * T
 
@@ -656,6 +664,10 @@ def main():
                    "tasks": T, "costs": list(costs), "device": info.name.decode(),
                    "main_kernel_us": round(main_us, 2), "zero_pass_us": round(zero_us, 2),
                    "per_task_mode_us": round(per_task_us, 2),
+                   "empty_rows": "C cleared once before the timed steps, as the reference "
+                                 "clears it outside its timed kernel; the steps write every "
+                                 "row with nonzeros and leave the rows without "
+                                 f"({n_empty} of {g.n}), as the reference's kernel does",
                    "host_pointer_call_ms": None if host_call_ms is None else round(host_call_ms, 1),
                    "preprocessing": prep,
                    "schedule": schedule,

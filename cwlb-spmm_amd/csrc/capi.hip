@@ -80,10 +80,11 @@ cwlb_status run_spmm(cwlb_ctx* ctx, const SpmmArgs& a, uint32_t flags, cwlb_timi
     DeviceGuard g(ctx->device);
     const bool zero_all = (flags & CWLB_SPMM_ZERO_OUTPUT) != 0;
     const bool per_task = (flags & CWLB_SPMM_PER_TASK) != 0;
+    const bool keep_empty = (flags & CWLB_SPMM_KEEP_EMPTY_ROWS) != 0;
     if (a.K == 0 || a.n_tasks == 0) {
         // The reference returns a zero matrix and time 0 (parallelMatrix.cpp:80-83, 101-104).
         if (zero_all && a.n_rows > 0 && a.K > 0) {
-            st = launch_spmm_mean(ctx, a, true, per_task, false);
+            st = launch_spmm_mean(ctx, a, true, per_task, keep_empty, false);
             if (st != CWLB_OK) return st;
         }
         if (timing) {
@@ -92,7 +93,7 @@ cwlb_status run_spmm(cwlb_ctx* ctx, const SpmmArgs& a, uint32_t flags, cwlb_timi
         }
         return CWLB_OK;
     }
-    st = launch_spmm_mean(ctx, a, zero_all, per_task, timing != nullptr);
+    st = launch_spmm_mean(ctx, a, zero_all, per_task, keep_empty, timing != nullptr);
     if (st != CWLB_OK) return st;
     if (timing) return finish_timed(ctx, timing);
     return CWLB_OK;

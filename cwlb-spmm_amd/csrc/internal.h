@@ -145,8 +145,10 @@ struct SpmmArgs {
 // Enqueues the split-row clearing pass (or the full clear when zero_all)
 // and the aggregation kernel on ctx->stream, bracketed by ctx->ev[0..2].
 // per_task runs one task per wave (no task-run fusion, no feature slices).
+// Rows without nonzeros are stored as zeros unless zero_all or keep_empty
+// (the caller's C holds zeros there already).
 cwlb_status launch_spmm_mean(cwlb_ctx* ctx, const SpmmArgs& a, bool zero_all, bool per_task,
-                             bool record_events);
+                             bool keep_empty, bool record_events);
 
 // Computes into ctx->d_run_order a permutation of the n_runs runs (runs of
 // M tasks) sorted by the original id of each run's first row, on

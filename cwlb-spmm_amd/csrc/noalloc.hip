@@ -115,12 +115,13 @@ extern "C" cwlb_status cwlb_spmm_mean_f32_noalloc(
     c.sched_xcd = 1;
     const bool zero_all = (flags & CWLB_SPMM_ZERO_OUTPUT) != 0;
     const bool per_task = (flags & CWLB_SPMM_PER_TASK) != 0;
+    const bool keep_empty = (flags & CWLB_SPMM_KEEP_EMPTY_ROWS) != 0;
     SpmmArgs a{row_ptr, col_idx, val, origin, n_rows, nnz, H, h_rows, K, tasks, n_tasks, C};
     if (K > 0 && n_tasks > 0) {
-        const cwlb_status s = launch_spmm_mean(&c, a, zero_all, per_task, false);
+        const cwlb_status s = launch_spmm_mean(&c, a, zero_all, per_task, keep_empty, false);
         if (s != CWLB_OK) return s;
     } else if (zero_all && n_rows > 0 && K > 0) {
-        const cwlb_status s = launch_spmm_mean(&c, a, true, per_task, false);
+        const cwlb_status s = launch_spmm_mean(&c, a, true, per_task, keep_empty, false);
         if (s != CWLB_OK) return s;
     }
     if (!synchronize) return CWLB_OK;

@@ -386,6 +386,8 @@ __device__ __forceinline__ void block_slice(int& slice, long long& jb, long long
 // band; first: the first phase; seq: the call's sequence number; status[1]
 // == seq marks a task list that is not a chain, which then runs in one pass
 // over ci / val in the first launch and not at all in the others).
+// write_empty: rows without nonzeros are stored as zeros; 0 leaves them to
+// the caller's clearing, as the reference's kernel never writes them.
 template <int VEC, int G, int R, int U, int SL, bool HN, bool O6, bool PH>
 __global__ void __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(O6 ? 6 : 1)))
 spmm_mean_runs(const int* __restrict__ rp, const int* __restrict__ ci,
@@ -396,7 +398,7 @@ spmm_mean_runs(const int* __restrict__ rp, const int* __restrict__ ci,
                const unsigned long long* __restrict__ hints, float* __restrict__ C,
                int* __restrict__ status, const int* __restrict__ pb,
                const int* __restrict__ pe, const int* __restrict__ ci_b,
-               const float* __restrict__ val_b, int first_phase, int seq)
+               const float* __restrict__ val_b, int first_phase, int seq, int write_empty)
 {
     static_assert(!HN || VEC == 4, "hinted gathers move 16 bytes per lane");
     using V = typename VecT<VEC>::T;
@@ -726,7 +728,7 @@ spmm_mean_runs(const int* __restrict__ rp, const int* __restrict__ ci,
                         }
                         float* crow = Cs + static_cast<size_t>(o) * ld;
                         if (cu.d == 0) {
-                            if (first) {
+                            if (first && write_empty) {
 #pragma unroll
                                 for (int q = 0; q < R; ++q) {
                                     const int f = fl + G * q;
@@ -979,6 +981,7 @@ struct Plan {
     const float* vb;  // and of the values
     int first;
     int seq;
+    int write_empty;  // store rows without nonzeros (as zeros)
 };
 
 // Launches one instantiation; returns its resident waves per CU at most
@@ -1001,7 +1004,8 @@ int launch_main(hipStream_t st, const SpmmArgs& a, const Plan& p, int* status)
                        a.col_idx, a.val, a.origin, a.n_rows, static_cast<long long>(a.nnz), a.H,
                        static_cast<long long>(a.h_rows), a.K, a.tasks,
                        static_cast<long long>(a.n_tasks), p.M, p.runs, p.blocks, p.chunk, p.order,
-                       p.hints, a.C, status, p.pb, p.pe, p.cb, p.vb, p.first, p.seq);
+                       p.hints, a.C, status, p.pb, p.pe, p.cb, p.vb, p.first, p.seq,
+                       p.write_empty);
     return waves_per_cu;
 }
 
@@ -1190,17 +1194,21 @@ Plan make_plan(const cwlb_ctx* ctx, const SpmmArgs& a, bool per_task)
     p.vb = nullptr;
     p.first = 1;
     p.seq = 0;
+    p.write_empty = 1;
     return p;
 }
 
 }  // namespace
 
 cwlb_status launch_spmm_mean(cwlb_ctx* ctx, const SpmmArgs& a, bool zero_all, bool per_task,
-                             bool record_events)
+                             bool keep_empty, bool record_events)
 {
     hipStream_t st = ctx->stream;
     (void)hipGetLastError();  // report only the launches below
     Plan p = make_plan(ctx, a, per_task);
+    // Rows without nonzeros hold zeros already when this call clears C, or
+    // when the caller says an earlier one did.
+    p.write_empty = zero_all || keep_empty ? 0 : 1;
     if (a.n_tasks > kMaxGridBlocks * kBlock && a.K > 0)
         return fail(CWLB_UNSUPPORTED, "spmm: more than 2^32 tasks");
     if (p.grid > kMaxGridBlocks && a.n_tasks > 0 && a.K > 0)

@@ -18,6 +18,7 @@ STATUS_NAMES = ["OK", "INVALID_ARG", "UNSUPPORTED", "HIP_ERROR", "OOM", "IO_ERRO
                 "INSUFFICIENT", "RUNTIME_ERROR"]
 ZERO_OUTPUT = 0x1
 PER_TASK = 0x2
+KEEP_EMPTY_ROWS = 0x4
 
 # Every function declared in include/cwlb.h (checked by the CPU tests).
 EXPORTS = [

@@ -218,8 +218,9 @@ SingleSResult run_single_s(cwlb::Device& queue, const CSR_Order& csr,
     for (int it = 0; it < LOOPCOUNT; ++it) {
         cwlb_timing t{};
         // The first launch clears all of C (the reference's zeroed output);
-        // later launches rewrite every row the partition covers.
-        const uint32_t flags = it == 0 ? CWLB_SPMM_ZERO_OUTPUT : 0u;
+        // later launches rewrite every row with nonzeros and, as the
+        // reference's kernel, leave the rows without nonzeros at that 0.
+        const uint32_t flags = it == 0 ? CWLB_SPMM_ZERO_OUTPUT : CWLB_SPMM_KEEP_EMPTY_ROWS;
         const auto fn = large_k ? cwlb_spmm_mean_f32_large_k : cwlb_spmm_mean_f32;
         cwlb::check(fn(queue.ctx(), d_rp.get(), d_ci.get(), d_v.get(), d_o.get(),
                        static_cast<int32_t>(rows), static_cast<int64_t>(nnz), d_h.get(),

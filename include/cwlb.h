@@ -288,6 +288,16 @@ cwlb_status cwlb_ctx_last_launch(cwlb_ctx* ctx, cwlb_launch_info* out);
  * one, starts a new stretch.  For task lists without overlapping tasks both
  * modes give the same result up to float rounding. */
 #define CWLB_SPMM_PER_TASK 0x2u
+/* Leave the rows without nonzeros unwritten: the caller's C holds zeros
+ * there already (an earlier call with CWLB_SPMM_ZERO_OUTPUT on the same C
+ * and row_ptr/origin, or a clear of its own).  This is what the reference's
+ * kernel does: it never writes such rows, and its C starts cleared
+ * (parallelMatrix.cpp:112, 166).  Without the flag they are stored as
+ * zeros, so that C needs no clearing; with CWLB_SPMM_ZERO_OUTPUT they are
+ * never stored either (the call has just cleared them).  No counterpart
+ * flag in the reference; for repeated calls on one C, where it saves one
+ * store per empty row (R-MAT 2^22: 52% of the rows). */
+#define CWLB_SPMM_KEEP_EMPTY_ROWS 0x4u
 
 cwlb_status cwlb_spmm_mean_f32(cwlb_ctx* ctx, const int32_t* row_ptr, const int32_t* col_idx,
                                const float* val, const int32_t* origin, int32_t n_rows,

@@ -47,6 +47,7 @@ def draw_case(i):
         # drawn from its own stream, so the other settings of a case do not
         # depend on it
         "phases": [0, 0, 2, 5, 16][int(np.random.default_rng(5000 + i).integers(5))],
+        "keep_empty": bool(np.random.default_rng(7000 + i).integers(3) == 0),
     }
 
 
@@ -87,9 +88,10 @@ def test_random_schedule_case(gpu_ctx, i):
     gpu_ctx.set_cache_hints(c["hot_rows"] * 4 * K)
     gpu_ctx.set_occupancy(c["occupancy"])
     gpu_ctx.set_column_phases(c["phases"])
+    flags = c["flags"] | (capi.KEEP_EMPTY_ROWS if c["keep_empty"] else 0)
     try:
         gpu_ctx.spmm(d_rp, d_ci, d_v, d_o, g.n, g.nnz, d_H, g.n, K, d_t, len(p.tasks), C,
-                     flags=c["flags"], large_k=large_k)
+                     flags=flags, large_k=large_k)
         info = gpu_ctx.last_launch()
     finally:
         gpu_ctx.set_schedule(0, 0)
@@ -104,6 +106,10 @@ def test_random_schedule_case(gpu_ctx, i):
         # the rows without nonzeros when their slot cost exceeds the capacity
         # (utils.cpp:972-976); the reference's cleared C holds 0 for them.
         ref[uncovered_rows(p.tasks, p.origin, g.n)] = np.nan
+        if c["keep_empty"]:
+            # Rows without nonzeros are left too (the reference's kernel
+            # skips them, parallelMatrix.cpp:166).
+            ref[p.origin[np.diff(p.row_ptr) == 0]] = np.nan
     np.testing.assert_allclose(C.cpu().numpy(), ref, rtol=RTOL, atol=ATOL, err_msg=str(c))
 
     per_task = bool(c["flags"] & capi.PER_TASK)

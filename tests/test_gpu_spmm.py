@@ -551,6 +551,42 @@ def test_zero_output_flag_with_partial_cover(gpu_ctx):
     check(got, ref32)
 
 
+@pytest.mark.parametrize("phases", [0, 3])
+@pytest.mark.parametrize("K", [32, 128, 1100])
+def test_keep_empty_rows_flag(gpu_ctx, sched, K, phases, rng):
+    """KEEP_EMPTY_ROWS leaves the rows without nonzeros as they were (the
+    reference's kernel skips them, parallelMatrix.cpp:166, and its C starts
+    cleared, :112); every other row gets the reference's result.  Without
+    the flag they are stored as zeros; with ZERO_OUTPUT (alone or with it)
+    they are the call's cleared 0.  About 60% of the rows are empty, among
+    rows of degree 1 to 3 and a hub row split over many tasks."""
+    n = 5000
+    deg = rng.integers(1, 4, n) * (rng.random(n) < 0.4)
+    deg[11] = 3000
+    rp = np.concatenate([[0], np.cumsum(deg)]).astype(np.int32)
+    ci = rng.integers(0, n, rp[-1]).astype(np.int32)
+    val = rng.uniform(-2, 2, rp[-1]).astype(np.float32)
+    g = custom_graph(rp, ci, val)
+    H = synth.features(n, K, 2)
+    p = problem(g, UNIT_COSTS, 8)
+    ref32 = oracle.spmm_mean_f32(p.row_ptr, p.col_idx, p.val, p.origin, H, p.tasks)
+    empty = p.origin[np.diff(p.row_ptr) == 0]
+    assert 0 < len(empty) < n
+    written = np.ones(n, bool)
+    written[empty] = False
+    large_k = K > 1024
+    gpu_ctx.set_column_phases(phases)
+    try:
+        got, _ = run_gpu(gpu_ctx, p, H, flags=sched | capi.KEEP_EMPTY_ROWS, large_k=large_k)
+        assert np.isnan(got[empty]).all()
+        check(got[written], ref32[written])
+        for f in (capi.ZERO_OUTPUT, capi.ZERO_OUTPUT | capi.KEEP_EMPTY_ROWS, 0):
+            got, _ = run_gpu(gpu_ctx, p, H, flags=sched | f, large_k=large_k)
+            check(got, ref32)
+    finally:
+        gpu_ctx.set_column_phases(0)
+
+
 def test_launch_grid_limit(gpu_ctx):
     """70M empty tasks: one task per wave (or a fixed run length of 1) would
     need more than 2^32 work-items and is refused before any launch; the

@@ -29,6 +29,14 @@ def test_library_exports_every_declared_function():
     assert sorted(capi.EXPORTS) == declared
 
 
+def test_flag_constants_match_header():
+    text = open(os.path.join(paths.INCLUDE_DIR, "cwlb.h")).read()
+    for name, value in [("ZERO_OUTPUT", capi.ZERO_OUTPUT), ("PER_TASK", capi.PER_TASK),
+                        ("KEEP_EMPTY_ROWS", capi.KEEP_EMPTY_ROWS)]:
+        m = re.search(rf"#define CWLB_SPMM_{name} (0x[0-9a-fA-F]+)u", text)
+        assert m and int(m.group(1), 16) == value, name
+
+
 def test_library_is_gfx950_only():
     """The shared object carries gfx950 code objects only."""
     data = open(capi.lib_path(), "rb").read()

@@ -62,7 +62,8 @@ def test_noalloc_matches_context_entry_twice(gpu_ctx):
 
 
 @pytest.mark.parametrize("flags,m,sl", [(0, 8, 2), (capi.ZERO_OUTPUT, 0, 0),
-                                        (capi.PER_TASK, 0, 0), (0, 64, 4)])
+                                        (capi.PER_TASK, 0, 0), (0, 64, 4),
+                                        (capi.KEEP_EMPTY_ROWS, 8, 2)])
 def test_noalloc_flags_and_schedule(gpu_ctx, flags, m, sl):
     import torch
     g, p, H, d, d_H, d_t = _inputs(torch, 4, 12, 64, 5, UNIT_COSTS)
