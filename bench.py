@@ -475,7 +475,8 @@ def main():
         if tuning:
             t0 = time.perf_counter()
             m, sl, (order, xcd) = tune(d_t, len(tk))
-            t_tune += time.perf_counter() - t0
+            rec["tuning_ms"] = round((time.perf_counter() - t0) * 1e3, 1)
+            t_tune += rec["tuning_ms"]
             rec["schedule"] = {"tasks_per_wave": m, "feature_slices": sl, "run_order": order,
                                "xcd_blocks": xcd, "hot_bytes": ctx.cache_hints(),
                                "occupancy": ctx.occupancy(), "phases": ctx.column_phases()}
@@ -503,7 +504,9 @@ def main():
                         phases=args.phases)
         log(f"fixed schedule: {schedule}")
     elif tuning:
-        schedule.update(tuned, tuned=True, tuning_ms=round(t_tune * 1e3, 1))
+        # One cwlb_ctx_tune_schedule call per S candidate (each candidate's
+        # own time is in s_candidates).
+        schedule.update(tuned, tuned=True, tuning_ms_all_candidates=round(t_tune, 1))
         log(f"tuned schedule: {schedule}")
 
     def apply(c, sched):

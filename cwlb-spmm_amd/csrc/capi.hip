@@ -509,8 +509,11 @@ cwlb_status cwlb_ctx_tune_schedule(cwlb_ctx* ctx, const int32_t* row_ptr, const 
     // One warm-up, then the median of `trials` event-timed calls under the
     // context's current settings.  The warm-up builds what the settings
     // need (run order, hints); `applies` (optional) reads the warm-up's
-    // launch and skips the timing when it returns false.
-    auto time_current = [&](float* med, bool (*applies)(const cwlb_ctx*)) -> cwlb_status {
+    // launch and skips the timing when it returns false.  A first timed
+    // call above `cutoff` (> 0) ends the timing: that call's time is
+    // returned, and a candidate 10% behind the best cannot win on noise.
+    auto time_current = [&](float* med, bool (*applies)(const cwlb_ctx*),
+                            float cutoff) -> cwlb_status {
         cwlb_status s = run_spmm(ctx, a, 0, nullptr);
         if (s != CWLB_OK) return s;
         if (applies && !applies(ctx)) {
@@ -521,6 +524,10 @@ cwlb_status cwlb_ctx_tune_schedule(cwlb_ctx* ctx, const int32_t* row_ptr, const 
             cwlb_timing tm{};
             s = run_spmm(ctx, a, 0, &tm);
             if (s != CWLB_OK) return s;
+            if (t == 0 && cutoff > 0.0f && tm.total_us > cutoff) {
+                *med = tm.total_us;
+                return CWLB_OK;
+            }
             times[static_cast<size_t>(t)] = tm.total_us;
         }
         std::sort(times.begin(), times.end());
@@ -542,7 +549,7 @@ cwlb_status cwlb_ctx_tune_schedule(cwlb_ctx* ctx, const int32_t* row_ptr, const 
         ctx->sched_tasks_per_wave = c.first;
         ctx->sched_slices = c.second;
         float med = 0.0f;
-        st = time_current(&med, nullptr);
+        st = time_current(&med, nullptr, best_us * 1.1f);
         if (st != CWLB_OK) {
             restore(keep_order, keep_xcd);
             return st;
@@ -570,7 +577,7 @@ cwlb_status cwlb_ctx_tune_schedule(cwlb_ctx* ctx, const int32_t* row_ptr, const 
                     ctx->sched_order = locs[i].first;
                     ctx->sched_xcd = locs[i].second;
                     float med = 0.0f;
-                    st = time_current(&med, nullptr);
+                    st = time_current(&med, nullptr, 0.0f);
                     if (st == CWLB_OK && (loc_us[i] == 0.0f || med < loc_us[i])) loc_us[i] = med;
                 }
             }
@@ -598,13 +605,13 @@ cwlb_status cwlb_ctx_tune_schedule(cwlb_ctx* ctx, const int32_t* row_ptr, const 
         // fresh timing.
         float base = 0.0f;
         const int m_standard = best.first;
-        st = time_current(&base, nullptr);
+        st = time_current(&base, nullptr, 0.0f);
         if (st == CWLB_OK) {
             ctx->sched_occupancy = 6;
             float med = 0.0f;
             st = time_current(&med, [](const cwlb_ctx* c) {
                 return c->last_launch.waves_per_simd == 6;
-            });
+            }, 0.0f);
             if (st == CWLB_OK && !(med > 0.0f && med < base)) ctx->sched_occupancy = 0;
             if (st == CWLB_OK && ctx->sched_occupancy == 6) {
                 // More waves in flight can move the best run length: its
@@ -614,7 +621,7 @@ cwlb_status cwlb_ctx_tune_schedule(cwlb_ctx* ctx, const int32_t* row_ptr, const 
                 for (int m : {m0 / 2, m0 * 2}) {
                     if (st != CWLB_OK || m0 == 0 || m < 1 || m > 64) continue;
                     ctx->sched_tasks_per_wave = m;
-                    st = time_current(&med, nullptr);
+                    st = time_current(&med, nullptr, 0.0f);
                     if (st == CWLB_OK && med < base) {
                         base = med;
                         best.first = m;
@@ -623,7 +630,7 @@ cwlb_status cwlb_ctx_tune_schedule(cwlb_ctx* ctx, const int32_t* row_ptr, const 
                 ctx->sched_tasks_per_wave = best.first;
             }
         }
-        if (st == CWLB_OK) st = time_current(&base, nullptr);
+        if (st == CWLB_OK) st = time_current(&base, nullptr, 0.0f);
         long long best_hot = 0;
         for (long long mb : {24ll, 48ll, 96ll}) {
             if (st != CWLB_OK) break;
@@ -631,7 +638,7 @@ cwlb_status cwlb_ctx_tune_schedule(cwlb_ctx* ctx, const int32_t* row_ptr, const 
             float med = 0.0f;
             // Hints that do not apply to this call (K, alignment, H size) or
             // mark no column cold leave nothing to time.
-            st = time_current(&med, [](const cwlb_ctx* c) { return c->last_call_hinted; });
+            st = time_current(&med, [](const cwlb_ctx* c) { return c->last_call_hinted; }, 0.0f);
             if (st != CWLB_OK || med == 0.0f) break;
             if (med < base) {
                 base = med;
@@ -644,11 +651,11 @@ cwlb_status cwlb_ctx_tune_schedule(cwlb_ctx* ctx, const int32_t* row_ptr, const 
             // the standard kernel (at its own run length) can be faster.
             // Both are timed afresh, one after the other.
             const int m6 = best.first;
-            if (best_hot) st = time_current(&base, nullptr);
+            if (best_hot) st = time_current(&base, nullptr, 0.0f);
             ctx->sched_occupancy = 0;
             ctx->sched_tasks_per_wave = m_standard;
             float med = 0.0f;
-            if (st == CWLB_OK) st = time_current(&med, nullptr);
+            if (st == CWLB_OK) st = time_current(&med, nullptr, 0.0f);
             if (st == CWLB_OK && med < base) {
                 best.first = m_standard;
             } else {
@@ -664,7 +671,7 @@ cwlb_status cwlb_ctx_tune_schedule(cwlb_ctx* ctx, const int32_t* row_ptr, const 
         // kept when faster than the settings so far, re-timed first.
         const long long h_bytes = h_rows * static_cast<long long>(K) * 4;
         if (st == CWLB_OK && h_bytes >= (512ll << 20) && nnz >= 64ll * n_rows && K % 4 == 0) {
-            st = time_current(&base, nullptr);
+            st = time_current(&base, nullptr, 0.0f);
             const long long hot_kept = ctx->sched_hot_bytes;
             const int occ_kept = ctx->sched_occupancy;
             int best_p = 0, best_pm = best.first, best_psl = best.second;
@@ -679,7 +686,7 @@ cwlb_status cwlb_ctx_tune_schedule(cwlb_ctx* ctx, const int32_t* row_ptr, const 
                         float med = 0.0f;
                         st = time_current(&med, [](const cwlb_ctx* c) {
                             return c->last_launch.column_phases > 1;
-                        });
+                        }, base * 1.1f);
                         if (st == CWLB_OK && med > 0.0f && med < base) {
                             base = med;
                             best_p = P;

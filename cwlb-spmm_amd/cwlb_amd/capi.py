@@ -104,12 +104,28 @@ def lib_path():
     return os.path.join(paths.LIB_DIR, "libcwlb.so")
 
 
+def _share_torch_hip_runtime():
+    """One HIP runtime per process.  torch ships its own libamdhip64 and
+    libhsa-runtime64 under the same sonames as ROCm's (libamdhip64.so.7,
+    libhsa-runtime64.so.1) and loads them by file name.  Loaded after this
+    library, which links ROCm's, they would form a second runtime in the
+    process, and whichever initialises the GPU second finds no device
+    ("no ROCm-capable device is detected").  Importing torch first makes
+    this library bind to the runtime torch has loaded, as it does whenever
+    torch is imported before it.  Without torch the library uses ROCm's."""
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
+
+
 def lib():
     global _LIB
     if _LIB is None:
         path = lib_path()
         if not os.path.exists(path):
             raise RuntimeError(f"{path} missing: build with __graft_entry__.build()")
+        _share_torch_hip_runtime()
         L = C.CDLL(path)
         L.cwlb_version.restype = C.c_char_p
         L.cwlb_last_error.restype = C.c_char_p

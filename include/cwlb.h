@@ -316,7 +316,9 @@ cwlb_status cwlb_spmm_mean_f32_large_k(cwlb_ctx* ctx, const int32_t* row_ptr,
  * schedule and under every tasks-per-wave value in {2, 4, ..., 64} with 1,
  * 2, 4 or 8 feature slices (slices of at least 32 floats), `trials`
  * event-timed calls each after one warm-up (median of split-row clearing +
- * aggregation), and sets
+ * aggregation; a run length or slice count, or later a phase setting,
+ * whose first timed call is more than 10% behind the best so far is not
+ * timed further), and sets
  * the fastest on the context (cwlb_ctx_set_schedule); the choice is also
  * returned through the optional out pointers (0, 0 = the automatic schedule
  * won).  With locality_out non-null (two int32), the fastest schedule is

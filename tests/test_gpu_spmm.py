@@ -11,11 +11,15 @@ do not need the CPU oracle over the whole graph: all-ones features give
 exactly 1 (unit values) or 0 (degree-0 rows), and sampled rows match the
 fp64 closed form.
 """
+import subprocess
+import sys
+import textwrap
+
 import numpy as np
 import pytest
 
 import oracle
-from conftest import SKEWED_COSTS, UNIT_COSTS
+from conftest import PKG, ROOT, SKEWED_COSTS, UNIT_COSTS
 from cwlb_amd import capi, paths, synth, workloads
 
 pytestmark = pytest.mark.gpu
@@ -585,6 +589,37 @@ def test_keep_empty_rows_flag(gpu_ctx, sched, K, phases, rng):
             check(got, ref32)
     finally:
         gpu_ctx.set_column_phases(0)
+
+
+def test_library_loaded_before_torch():
+    """A fresh process that calls the library's host functions before it
+    imports torch still gets a working context.  torch's own HIP runtime
+    shares ROCm's sonames; had it been loaded after this library, the
+    process would hold two runtimes and the second to initialise would find
+    no device.  The binding imports torch before it loads the library."""
+    code = textwrap.dedent(f"""
+        import sys
+        sys.path[:0] = [{ROOT!r}, {PKG!r}]
+        import numpy as np
+        import oracle
+        from cwlb_amd import capi, synth, workloads
+        assert "torch" not in sys.modules
+        g = workloads.small(1, seed=3)
+        p = workloads.prepare(g, {UNIT_COSTS!r}, 6)  # host calls load the library
+        import torch
+        H = synth.features(g.n, 32, 1)
+        dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+        C = torch.full((g.n, 32), float("nan"), device="cuda")
+        ctx = capi.Context(0, torch.cuda.current_stream().cuda_stream)
+        ctx.spmm(dev(p.row_ptr), dev(p.col_idx), dev(p.val), dev(p.origin), g.n, g.nnz,
+                 dev(H), g.n, 32, dev(p.tasks.reshape(-1)), len(p.tasks), C)
+        ref = oracle.spmm_mean_f32(p.row_ptr, p.col_idx, p.val, p.origin, H, p.tasks)
+        np.testing.assert_allclose(C.cpu().numpy(), ref, rtol={RTOL!r}, atol={ATOL!r})
+        ctx.close()
+        print("OK", flush=True)
+    """)
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=240)
+    assert r.returncode == 0 and "OK" in r.stdout, r.stdout[-2000:] + r.stderr[-2000:]
 
 
 def test_launch_grid_limit(gpu_ctx):
