@@ -9,6 +9,10 @@ wave-based candidates as the reference's --candidates mode does.
 A step is one SpMM call (split-row clearing + aggregation kernel) over the
 whole graph with all inputs resident in HBM.  W warm-up steps, then K timed
 steps between synchronisations, timed with HIP events on the launch stream.
+C is cleared once before the steps, as the reference clears its output
+outside its timed kernel; every step rewrites each row with nonzeros and,
+as the reference's kernel, leaves the rows without nonzeros at that 0
+(CWLB_SPMM_KEEP_EMPTY_ROWS).
 
 Prints one JSON line: GFLOP/s (2 nnz K / t) as `value`; the aggregation
 kernel's roofline: the HBM-side traffic of one launch, measured with
