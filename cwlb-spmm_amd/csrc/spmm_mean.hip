@@ -7,7 +7,9 @@
 //     acc[k] = sum_j val[j] * H[col[j]][k]   (fma, CSR order per lane)
 // divides by the FULL degree, then stores C[origin[r]] for a full row or
 // adds atomically for a partial one.  Rows of degree 0 are written as zeros
-// (the reference leaves its host-zeroed C untouched there).
+// unless C holds zeros there already (the call clears C, or the caller says
+// an earlier clear did): the reference leaves its host-zeroed C untouched
+// there.
 //
 // Mapping to CDNA4 (64-lane waves):
 //   * a wave executes a run of M consecutive tasks (M = 1 reproduces the
