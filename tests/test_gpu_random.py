@@ -9,6 +9,8 @@ bar: every output row within 1e-5 relative / 1e-6 absolute of the oracle in
 the reference's value order, and the schedule the library reports for the
 launch consistent with the settings.  The reference's kernel is
 src/parallelMatrix.cpp:63-254 (K <= 1024) and :264-683 (larger K).
+Further drawn cases go through the host-pointer entry (shuffled lists
+included) and the allocation-free entry (drawn flags, run length, slices).
 """
 import numpy as np
 import pytest
@@ -142,3 +144,59 @@ def test_random_schedule_case(gpu_ctx, i):
     assert info["waves_per_simd"] == (6 if o6 else 0), (info, c)
     if phased:
         assert info["cache_hints"] == 0, (info, c)
+
+
+N_ENTRY_CASES = 64
+
+
+def entry_case(i):
+    """A drawn case's graph, prepared problem and features (seeds apart from
+    the device-entry cases)."""
+    c = draw_case(300000 + i)
+    g = workloads.small(c["family"], seed=c["seed"])
+    p = workloads.prepare(g, c["costs"], c["S"])
+    H = synth.features(g.n, c["K"], c["seed"] % 997)
+    return c, g, p, H
+
+
+@pytest.mark.parametrize("i", range(N_ENTRY_CASES))
+def test_random_host_entry_case(gpu_ctx, i):
+    """The host-pointer entry (the drop-in spmmKernel): always the
+    reference's zeroed C; a shuffled list (about a third of the cases) is
+    run one task per wave, as it does not tile the nonzeros in order."""
+    c, g, p, H = entry_case(i)
+    r = np.random.default_rng(400000 + i)
+    tasks = np.asarray(p.tasks, np.int32).reshape(-1, 4)
+    if len(tasks) and r.random() < 0.3:
+        tasks = tasks[r.permutation(len(tasks))]
+    print(f"case {i}: {c} shuffled={not np.array_equal(tasks, p.tasks)}", flush=True)
+    got, _ = gpu_ctx.spmm_host(p.row_ptr, p.col_idx, p.val, p.origin, H, tasks)
+    ref = oracle.spmm_mean_f32(p.row_ptr, p.col_idx, p.val, p.origin, H, tasks)
+    np.testing.assert_allclose(got, ref, rtol=RTOL, atol=ATOL, err_msg=str(c))
+
+
+@pytest.mark.parametrize("i", range(N_ENTRY_CASES))
+def test_random_noalloc_entry_case(gpu_ctx, i):
+    """The allocation-free entry with drawn flags, run length and slices."""
+    import torch
+    c, g, p, H = entry_case(i)
+    r = np.random.default_rng(500000 + i)
+    flags = [0, capi.ZERO_OUTPUT, capi.PER_TASK, capi.KEEP_EMPTY_ROWS,
+             capi.ZERO_OUTPUT | capi.KEEP_EMPTY_ROWS][int(r.integers(5))]
+    m = [0, 1, 2, 8, 64][int(r.integers(5))]
+    sl = [0, 1, 2, 4, 8][int(r.integers(5))]
+    K = c["K"]
+    print(f"case {i}: {c} flags={flags} m={m} sl={sl}", flush=True)
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()  # noqa: E731
+    tk = np.ascontiguousarray(p.tasks, np.int32).reshape(-1)
+    C = torch.full((g.n, K), float("nan"), dtype=torch.float32, device="cuda")
+    capi.spmm_noalloc(torch.cuda.current_stream().cuda_stream, dev(p.row_ptr), dev(p.col_idx),
+                      dev(p.val), dev(p.origin), g.n, g.nnz, dev(H), g.n, K,
+                      dev(tk if tk.size else np.zeros(4, np.int32)), len(p.tasks), C,
+                      flags=flags, tasks_per_wave=m, feature_slices=sl)
+    ref = oracle.spmm_mean_f32(p.row_ptr, p.col_idx, p.val, p.origin, H, p.tasks)
+    if not flags & capi.ZERO_OUTPUT:
+        ref[uncovered_rows(p.tasks, p.origin, g.n)] = np.nan
+        if flags & capi.KEEP_EMPTY_ROWS:
+            ref[p.origin[np.diff(p.row_ptr) == 0]] = np.nan
+    np.testing.assert_allclose(C.cpu().numpy(), ref, rtol=RTOL, atol=ATOL, err_msg=str(c))
