@@ -39,20 +39,38 @@ __device__ __forceinline__ int band_of(int c, long long h_rows, int P)
     return (c < 0 || c >= h_rows) ? 0 : c % P;
 }
 
+// Lanes of one band: with one ballot per bit of the band numbers (bits
+// ballots, nb of them), the lanes whose band equals `band` are those that
+// agree with it on every bit.  mine: the lanes of this lane's band; lane_q:
+// the lanes of band `lane` (lane q's own band q), for the per-band counts.
+__device__ __forceinline__ void band_masks(int band, int nb, unsigned long long& mine,
+                                           unsigned long long& lane_q)
+{
+    const int lane = threadIdx.x & 63;
+    mine = ~0ull;
+    lane_q = ~0ull;
+    for (int b = 0; b < nb; ++b) {
+        const unsigned long long bb = __ballot((band >> b) & 1);
+        mine &= ((band >> b) & 1) ? bb : ~bb;
+        lane_q &= ((lane >> b) & 1) ? bb : ~bb;
+    }
+}
+
 // One wave per row (grid-stride), in batches of kBatch chunks of 64
 // nonzeros whose loads are all issued before any is used.
-//   * Counting pass: one ballot per band per chunk; lane q keeps band q's
-//     count in the row, and for a row of one batch (at most 64 * kBatch
-//     nonzeros) also band q's count before each chunk, while each lane
-//     keeps its nonzero's rank among the chunk's nonzeros of its band.  The
-//     bounds B_q(r), q in [1, P), are an exclusive scan of the counts.
+//   * Counting pass: per chunk, the bit-sliced band masks above (one ballot
+//     per bit of P, not one per band); lane q keeps band q's count in the
+//     row, and for a row of one batch (at most 64 * kBatch nonzeros) also
+//     band q's count before each chunk, while each lane keeps its nonzero's
+//     rank among the chunk's nonzeros of its band.  The bounds B_q(r), q in
+//     [1, P), are an exclusive scan of the counts.
 //   * A row of one batch keeps its columns and values in registers: each
 //     goes to its band's start + the band's count before its chunk + its
 //     rank (one shuffle per chunk), into the wave's LDS buffer, and the row
 //     is written out with coalesced stores.
 //   * A longer row is read again and scattered straight to memory, each
-//     nonzero to its band's next free slot (one ballot and one shuffle per
-//     band per chunk; lane q holds band q's next free position).
+//     nonzero to its band's next free slot (the band masks and one shuffle
+//     per chunk; lane q holds band q's next free position).
 // A row whose offsets leave [0, nnz] or decrease gets bounds 0 and no copy
 // (the aggregation skips and reports it).  Row positions are 64-bit: a row
 // may end within 64 of 2^31.
@@ -68,6 +86,7 @@ band_sort(const int* __restrict__ rp, const int* __restrict__ ci, const float* _
     const int lane = threadIdx.x & 63;
     const int wv = threadIdx.x >> 6;
     const unsigned long long below = (1ull << lane) - 1ull;  // lanes before this one
+    const int nb = 32 - __clz(P);  // bits of 0..P (P marks lanes past the row)
     const long long waves = static_cast<long long>(gridDim.x) * kWavesPerBlock;
     for (long long r = static_cast<long long>(blockIdx.x) * kWavesPerBlock + wv; r < n_rows;
          r += waves) {
@@ -96,11 +115,10 @@ band_sort(const int* __restrict__ rp, const int* __restrict__ ci, const float* _
                     const long long j = b0 + 64 * k + lane;
                     const int band = j < p1 ? band_of(c[k], h_rows, P) : P;
                     before[k] = tot;
-                    for (int q = 0; q < P; ++q) {
-                        const unsigned long long m = __ballot(band == q);
-                        if (band == q) rank[k] = __popcll(m & below);
-                        if (lane == q) tot += __popcll(m);
-                    }
+                    unsigned long long mine, lane_q;
+                    band_masks(band, nb, mine, lane_q);
+                    rank[k] = __popcll(mine & below);
+                    if (lane < P) tot += __popcll(lane_q);
                 }
             }
         }
@@ -159,14 +177,10 @@ band_sort(const int* __restrict__ rp, const int* __restrict__ ci, const float* _
                 const long long j = b0 + 64 * k + lane;
                 const bool in = j < p1;
                 const int band = in ? band_of(c[k], h_rows, P) : P;
-                int dst = 0;
-                for (int q = 0; q < P; ++q) {
-                    const unsigned long long m = __ballot(band == q);
-                    if (!m) continue;
-                    const int base = __shfl(next, q);
-                    if (band == q) dst = base + __popcll(m & below);
-                    if (lane == q) next += __popcll(m);
-                }
+                unsigned long long mine, lane_q;
+                band_masks(band, nb, mine, lane_q);
+                const int dst = __shfl(next, band) + __popcll(mine & below);
+                if (lane < P) next += __popcll(lane_q);
                 if (in) {
                     ci_out[dst] = c[k];
                     val_out[dst] = v[k];

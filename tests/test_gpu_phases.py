@@ -57,10 +57,13 @@ def device_band_sort(ctx, rp, ci, val, h_rows, P):
             vals.cpu().numpy()[:nnz])
 
 
-@pytest.mark.parametrize("P", [2, 3, 16, 64])
+@pytest.mark.parametrize("P", [2, 3, 5, 12, 16, 33, 63, 64])
 def test_band_sort_matches_host(gpu_ctx, P):
-    """Sorted and unsorted rows, columns below 0 and at or past h_rows, a
-    row of 3000 nonzeros (many 64-wide steps) and empty rows: the device
+    """Sorted and unsorted rows, columns below 0 and at or past h_rows,
+    rows of 512, 513, 700 and 3000 nonzeros (one batch of loads exactly,
+    and more: those are scattered straight to memory), empty rows, and band
+    counts at each width of the band number (P = 3, 5, 12, 33, 63, 64:
+    2 to 7 bits with the past-the-row marker): the device
     bounds and band-sorted copy equal the host restatement exactly (the
     copy is stable within each band).  Rows whose offsets leave [0, nnz] or
     decrease get bounds 0."""
@@ -68,7 +71,8 @@ def test_band_sort_matches_host(gpu_ctx, P):
     n, h = 2000, 777
     deg = rng.integers(0, 90, n)
     deg[5] = 3000
-    deg[rng.integers(0, n, 200)] = 0
+    deg[6:9] = (512, 513, 700)
+    deg[rng.integers(10, n, 200)] = 0
     rp = np.concatenate([[0], np.cumsum(deg)]).astype(np.int32)
     ci = rng.integers(-3, h + 4, rp[-1]).astype(np.int32)
     val = rng.normal(size=rp[-1]).astype(np.float32)
