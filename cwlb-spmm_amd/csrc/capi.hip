@@ -75,6 +75,7 @@ cwlb_status finish_timed(cwlb_ctx* ctx, cwlb_timing* timing)
 
 cwlb_status run_spmm(cwlb_ctx* ctx, const SpmmArgs& a, uint32_t flags, cwlb_timing* timing)
 {
+    if (flags & ~kSpmmFlags) return fail(CWLB_INVALID_ARG, "spmm: unknown flag bits");
     cwlb_status st = check_spmm_args(ctx, a);
     if (st != CWLB_OK) return st;
     DeviceGuard g(ctx->device);

@@ -142,6 +142,10 @@ struct SpmmArgs {
     float* C;
 };
 
+// Every flag bit the aggregation entry points take; others are rejected.
+constexpr uint32_t kSpmmFlags =
+    CWLB_SPMM_ZERO_OUTPUT | CWLB_SPMM_PER_TASK | CWLB_SPMM_KEEP_EMPTY_ROWS;
+
 // Enqueues the split-row clearing pass (or the full clear when zero_all)
 // and the aggregation kernel on ctx->stream, bracketed by ctx->ev[0..2].
 // per_task runs one task per wave (no task-run fusion, no feature slices).

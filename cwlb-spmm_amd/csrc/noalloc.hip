@@ -83,6 +83,7 @@ extern "C" cwlb_status cwlb_spmm_mean_f32_noalloc(
     DeviceSlot& slot = g_slots[device];
     std::call_once(slot.once, [&] { init_slot(slot, device); });
     if (slot.st != CWLB_OK) return fail(slot.st, slot.err);
+    if (flags & ~kSpmmFlags) return fail(CWLB_INVALID_ARG, "spmm: unknown flag bits");
     if (tasks_per_wave < 0 || tasks_per_wave > (1 << 20))
         return fail(CWLB_INVALID_ARG,
                     "tasks_per_wave must be in [0, 1048576] (0 = automatic)");

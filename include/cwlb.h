@@ -298,6 +298,8 @@ cwlb_status cwlb_ctx_last_launch(cwlb_ctx* ctx, cwlb_launch_info* out);
  * flag in the reference; for repeated calls on one C, where it saves one
  * store per empty row (R-MAT 2^22: 52% of the rows). */
 #define CWLB_SPMM_KEEP_EMPTY_ROWS 0x4u
+/* The aggregation entry points return CWLB_INVALID_ARG for any other flag
+ * bit. */
 
 cwlb_status cwlb_spmm_mean_f32(cwlb_ctx* ctx, const int32_t* row_ptr, const int32_t* col_idx,
                                const float* val, const int32_t* origin, int32_t n_rows,

@@ -591,6 +591,30 @@ def test_keep_empty_rows_flag(gpu_ctx, sched, K, phases, rng):
         gpu_ctx.set_column_phases(0)
 
 
+def test_unknown_flag_bits_are_rejected(gpu_ctx):
+    """Flag bits beyond the three defined are an argument error on the
+    context entry and on the allocation-free entry; nothing is written."""
+    import torch
+    g = workloads.small(1, seed=4)
+    p = problem(g, UNIT_COSTS, 6)
+    H = synth.features(g.n, 32, 2)
+    d = [dev(x) for x in (p.row_ptr, p.col_idx, p.val, p.origin, H,
+                          np.ascontiguousarray(p.tasks, np.int32).reshape(-1))]
+    C = torch.full((g.n, 32), float("nan"), dtype=torch.float32, device="cuda")
+    for bit in (0x8, 0x80000000):
+        with pytest.raises(capi.CwlbError) as e:
+            gpu_ctx.spmm(d[0], d[1], d[2], d[3], g.n, g.nnz, d[4], g.n, 32, d[5], len(p.tasks), C,
+                         flags=bit | capi.ZERO_OUTPUT)
+        assert e.value.status == capi.INVALID_ARG and "flag" in str(e.value)
+        with pytest.raises(capi.CwlbError) as e:
+            capi.spmm_noalloc(torch.cuda.current_stream().cuda_stream, d[0], d[1], d[2], d[3], g.n,
+                              g.nnz, d[4], g.n, 32, d[5], len(p.tasks), C, flags=bit)
+        assert e.value.status == capi.INVALID_ARG and "flag" in str(e.value)
+    assert torch.isnan(C).all()
+    got, _ = run_gpu(gpu_ctx, p, H, flags=capi.ZERO_OUTPUT | capi.PER_TASK | capi.KEEP_EMPTY_ROWS)
+    check(got, oracle.spmm_mean_f32(p.row_ptr, p.col_idx, p.val, p.origin, H, p.tasks))
+
+
 def test_library_loaded_before_torch():
     """A fresh process that calls the library's host functions before it
     imports torch still gets a working context.  torch's own HIP runtime
