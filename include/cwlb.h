@@ -261,8 +261,8 @@ cwlb_status cwlb_ctx_last_launch(cwlb_ctx* ctx, cwlb_launch_info* out);
  * (parallelMatrix.cpp:80-83, 101-104).
  * timing may be NULL (asynchronous: the bad entries above are then
  * reported by the next cwlb_ctx_synchronize); otherwise the call
- * synchronises.  The default and CWLB_SPMM_ZERO_OUTPUT paths launch kernels
- * only (no memset nodes, no allocation), so an asynchronous call can be
+ * synchronises.  With any of the flags a call launches kernels only (no
+ * memset nodes, no allocation), so an asynchronous call can be
  * captured into a HIP graph.  Under capture the run order (run_order = 2)
  * and the cache hints are reused when an earlier call built them for the
  * same arrays, and otherwise left out (task order, normal cache policy);
