@@ -1161,6 +1161,8 @@ HOT64 = 64 * 4 * 64
 CAPTURE_CASES = {
     "default": (0, (0, 0), (0, 0), (0, 1)),
     "zero_output": (capi.ZERO_OUTPUT, (0, 0), (0, 0), (0, 1)),
+    # the captured clear gives the empty rows the kernel leaves their zeros
+    "zero_output_keep_empty": (capi.ZERO_OUTPUT | capi.KEEP_EMPTY_ROWS, (0, 0), (0, 0), (0, 1)),
     "cache_hints_built": (0, (HOT64, 0), (HOT64, 0), (1, 1)),
     "cache_hints_unbuilt": (0, (2 * HOT64, 0), (HOT64, 0), (0, 1)),
     "run_order_built": (0, (0, 2), (0, 2), (0, 2)),
