@@ -114,7 +114,7 @@ def test_algorithmic_bytes_formula():
 
 def test_compulsory_bytes_formula():
     """CSR once, each referenced feature row once, C once: the R-MAT bound
-    with every row referenced is the 4.85 GB of the baseline table."""
+    with every row referenced is 4.85 GB (CSR, H and C once each)."""
     from cwlb_amd import workloads
     n, nnz, K = 4194304, 65245138, 128
     b = workloads.compulsory_bytes(n, n, nnz, K)
