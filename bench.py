@@ -15,13 +15,17 @@ as the reference's kernel, leaves the rows without nonzeros at that 0
 (CWLB_SPMM_KEEP_EMPTY_ROWS).
 
 Prints one JSON line: GFLOP/s (2 nnz K / t) as `value`; the aggregation
-kernel's roofline: the HBM-side traffic of one launch, measured with
-rocprofv3 counters on a replay of the very launch that was timed (child
-processes running this file with --pmc-child), over the kernel's mean
-event-timed duration, against 8 TB/s, next to the algorithmic and
-compulsory bytes per launch, the L2 hit rate and the occupancy; and the CPU
+kernel's roofline: the L2-to-fabric traffic of one launch (rocprofv3
+FETCH_SIZE + WRITE_SIZE; Infinity Cache hits are included, so it is an
+upper bound on the HBM bytes), measured on a replay of the very launch that
+was timed (child processes running this file with --pmc-child), over the
+kernel's mean event-timed duration, against 8 TB/s, next to the algorithmic
+and compulsory bytes per launch, the L2 hit rate and the occupancy; the CPU
 baseline (the reference kernel's semantics restated with OpenMP, on this
-host's cores, over a sample of the tasks).
+host's cores, over a sample of the tasks); and the parity of the timed
+launch: the whole of C after the last timed step against the oracle, at
+1e-5 relative / 1e-6 absolute per element.  Exits with status 1, after the
+line, when that check fails.
 """
 import argparse
 import csv
@@ -216,7 +220,8 @@ def pmc_child(args):
 
 
 def roofline_record(counters, err, b_alg, b_min, main_us, launched):
-    """The roofline object: measured HBM-side traffic per launch over the
+    """The roofline object: measured traffic per launch (L2-to-fabric bytes,
+    Infinity Cache hits included: an upper bound on the HBM bytes) over the
     kernel's mean duration against 8 TB/s, with the algorithmic and
     compulsory bytes beside it."""
     t = main_us * 1e-6
@@ -241,6 +246,8 @@ def roofline_record(counters, err, b_alg, b_min, main_us, launched):
     rec.update({
         "achieved": round(achieved, 1), "frac": round(achieved / HBM_PEAK_GBS, 4),
         "traffic": round(traffic), "traffic_read": round(read_b), "traffic_write": round(write_b),
+        "traffic_kind": "L2-to-fabric bytes (FETCH_SIZE + WRITE_SIZE), Infinity Cache hits "
+                        "included: an upper bound on the HBM bytes",
         "kernel": kernel_template(counters["name"]),
         "l2_hit_rate": None if not hits else round(hits / (hits + misses), 4),
         "waves_per_cu": None if k.get("MeanOccupancyPerCU") is None
@@ -254,6 +261,52 @@ def roofline_record(counters, err, b_alg, b_min, main_us, launched):
                             "timed launch in a child process; scales from a 1 GiB "
                             "device-to-device copy in the same runs"}})
     return rec
+
+
+# ------------------------------------------------------------------- parity
+RTOL, ATOL = 1e-5, 1e-6  # per element: |C - ref| <= ATOL + RTOL |ref|
+PARITY_COLS = 256  # feature columns per oracle block
+
+
+def parity_check(torch, C, H, rp, ci, val, origin, tasks, threads):
+    """The whole of C, as the timed launch left it, against the oracle (the
+    reference kernel's semantics, parallelMatrix.cpp:148-236: per task row
+    chunk, fp32 FMA sum in nonzero order, divided by the full row degree,
+    stored for whole rows and added atomically for split rows) on the same
+    device-resident H, at ATOL + RTOL |ref| per element.  Mean aggregation
+    is independent per feature column, so the oracle runs on blocks of
+    PARITY_COLS columns of H copied back from the device, and each block is
+    compared on the device.  Returns the record for the JSON line."""
+    import numpy as np
+
+    import oracle
+    n, K = C.shape
+    t0 = time.perf_counter()
+    worst, nan_rows, oracle_s = -float("inf"), 0, 0.0
+    for j0 in range(0, K, PARITY_COLS):
+        j1 = min(K, j0 + PARITY_COLS)
+        Hb = np.ascontiguousarray(H[:, j0:j1].cpu().numpy())
+        t1 = time.perf_counter()
+        ref = oracle.spmm_mean_f32_omp(rp, ci, val, origin, Hb, tasks, threads)
+        oracle_s += time.perf_counter() - t1
+        del Hb
+        ref_dev = torch.from_numpy(ref).to(C.device)
+        del ref
+        for r0 in range(0, n, 1 << 20):
+            c = C[r0:r0 + (1 << 20), j0:j1]
+            r = ref_dev[r0:r0 + (1 << 20)]
+            nan_rows += int(torch.isnan(c).any(dim=1).sum().item())
+            excess = ((c - r).abs() - (ATOL + RTOL * r.abs())).max().item()
+            worst = max(worst, excess)
+        del ref_dev
+    ok = nan_rows == 0 and worst <= 0.0
+    return {"ok": ok, "max_excess": worst, "nan_rows": nan_rows,
+            "elements": int(n) * int(K), "rtol": RTOL, "atol": ATOL,
+            "oracle_threads": threads, "oracle_s": round(oracle_s, 2),
+            "check_s": round(time.perf_counter() - t0, 2),
+            "how": "whole C after the last timed step, against the oracle's OpenMP "
+                   "restatement of the reference kernel on the same H and task list, "
+                   f"in blocks of {PARITY_COLS} feature columns"}
 
 
 # ------------------------------------------------------------ preprocessing
@@ -533,6 +586,13 @@ def main():
     e1.record(stream)
     torch.cuda.synchronize()
     ms_per_step = e0.elapsed_time(e1) / args.steps
+    # Outside the timed region: the output of the last timed step, checked
+    # whole against the oracle (the launch and schedule it ran with beside).
+    timed_launch = ctx.last_launch()
+    parity = parity_check(torch, C, H, rp, ci, val, origin, tasks, oracle.max_threads())
+    parity["launch"] = {"S": S, **timed_launch}
+    log(f"parity of the timed launch: ok={parity['ok']} max_excess={parity['max_excess']:.3g} "
+        f"({parity['check_s']} s)")
     # Per-kernel durations: the reference protocol (event-timed launches).
     times = [call(d_t, T, True) for _ in range(args.steps)]
     main_us = float(np.mean([t.main_us for t in times]))
@@ -682,8 +742,12 @@ def main():
                    **({"s_sweep": s_sweep} if s_sweep else {})},
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "parity": parity,
     }
     print(json.dumps(out), flush=True)
+    if not parity["ok"]:
+        log("the timed launch's C does not match the oracle")
+        sys.exit(1)
 
 
 if __name__ == "__main__":

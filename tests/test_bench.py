@@ -1,6 +1,8 @@
 """bench.py's host-side helpers (no GPU): the roofline record computed from
 counter values, the counter CSV reader, the launch arguments handed to the
-counter passes, and the algorithmic / compulsory byte formulas."""
+counter passes, the algorithmic / compulsory byte formulas, and the check of
+the timed launch's C against the oracle (on CPU tensors, with planted
+mistakes in C)."""
 import importlib
 import os
 import subprocess
@@ -120,3 +122,52 @@ def test_compulsory_bytes_formula():
     b = workloads.compulsory_bytes(n, n, nnz, K)
     assert b == 4 * (n + 1) + 8 * nnz + 4 * n * K + 4 * n * K + 4 * n
     assert 4.8e9 < b < 4.9e9
+
+
+def _parity_case(K):
+    """A small graph, its task list and the oracle's output at width K."""
+    import numpy as np
+
+    import oracle
+    from cwlb_amd import synth, workloads
+    g = workloads.small(4, seed=7)
+    p = workloads.prepare(g, (0.125, 1.375, 0.75, 3.5), S=8)
+    H = synth.features(g.n, K, 11)
+    ref = oracle.spmm_mean_f32(p.row_ptr, p.col_idx, p.val, p.origin, H, p.tasks)
+    return p, H, ref
+
+
+@pytest.mark.parametrize("cols", [256, 7])
+def test_parity_check_accepts_the_oracle_output(bench, monkeypatch, cols):
+    """The bench's own check of the timed launch (whole C against the oracle,
+    in blocks of feature columns) passes on the sequential oracle's output,
+    also when the columns fall into several blocks."""
+    import torch
+    monkeypatch.setattr(bench, "PARITY_COLS", cols)
+    p, H, ref = _parity_case(20)
+    rec = bench.parity_check(torch, torch.from_numpy(ref.copy()), torch.from_numpy(H), p.row_ptr,
+                             p.col_idx, p.val, p.origin, p.tasks, 2)
+    assert rec["ok"] and rec["max_excess"] <= 0.0 and rec["nan_rows"] == 0
+    assert rec["elements"] == ref.size
+
+
+@pytest.mark.parametrize("plant", ["offset", "nan", "zero_row"])
+def test_parity_check_rejects_a_wrong_c(bench, monkeypatch, plant):
+    """A C off by a few ulps beyond the tolerance in one element of the last
+    column block, a NaN, or one aggregated row left at zero fails the check."""
+    import numpy as np
+    import torch
+    monkeypatch.setattr(bench, "PARITY_COLS", 8)
+    p, H, ref = _parity_case(20)
+    bad = ref.copy()
+    deg = np.diff(p.row_ptr)[np.argsort(p.origin)]
+    r = int(np.flatnonzero(deg > 0)[3])
+    if plant == "offset":
+        bad[r, 19] += 2e-6 + 2e-5 * abs(bad[r, 19])
+    elif plant == "nan":
+        bad[r, 19] = np.nan
+    else:
+        bad[r, :] = 0.0
+    rec = bench.parity_check(torch, torch.from_numpy(bad), torch.from_numpy(H), p.row_ptr,
+                             p.col_idx, p.val, p.origin, p.tasks, 2)
+    assert not rec["ok"], rec
