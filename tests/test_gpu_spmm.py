@@ -6,10 +6,11 @@ Every case runs the C ABI (libcwlb.so) on an MI355X and compares with
   * oracle.spmm_mean_f64: the closed form (A H)[i] / deg(i) on the original
     CSR, independent of the permutation and the partition.
 Tolerance (from the parity contract): |gpu - ref| <= 1e-6 + 1e-5 * |ref|
-per element.  Full-size configurations are checked through properties that
-do not need the CPU oracle over the whole graph: all-ones features give
-exactly 1 (unit values) or 0 (degree-0 rows), and sampled rows match the
-fp64 closed form.
+per element.  Full-size configurations are checked on the whole of C
+against the OpenMP form of the reference-order oracle (the large-K widths in
+blocks of feature columns, since each column aggregates independently), and
+through properties: all-ones features give exactly 1 (unit values) or 0
+(degree-0 rows), and sampled rows match the fp64 closed form.
 """
 import subprocess
 import sys
@@ -265,14 +266,32 @@ def test_full_config_properties(gpu_ctx, cfg, per_task):
     print(f"cfg={cfg} total_us={t.total_us:.1f} zero_us={t.zero_us:.1f}", flush=True)
 
 
-@pytest.mark.parametrize("K", [1028, 2048])
-def test_full_chunglu_large_k_properties(gpu_ctx, K):
+def _whole_c_vs_oracle_in_column_blocks(torch, C, H, p, what, cols=1024):
+    """The whole of C against the reference-order oracle, one block of
+    feature columns at a time: mean aggregation is independent per column,
+    so the oracle on columns j0:j1 of H (copied back from the device) is the
+    oracle's value for those columns of C.  Keeps host buffers at n x cols."""
+    K = C.shape[1]
+    for j0 in range(0, K, cols):
+        j1 = min(K, j0 + cols)
+        Hb = np.ascontiguousarray(H[:, j0:j1].cpu().numpy())
+        ref = oracle.spmm_mean_f32_omp(p.row_ptr, p.col_idx, p.val, p.origin, Hb, p.tasks)
+        del Hb
+        ref_dev = torch.from_numpy(ref).cuda()
+        del ref
+        _assert_close_on_device(torch, C[:, j0:j1], ref_dev, f"{what} columns {j0}:{j1}")
+        del ref_dev
+
+
+@pytest.mark.parametrize("K", [1028, 4096])
+def test_full_chunglu_large_k_vs_oracle(gpu_ctx, K):
     """The large-K entry (K above the 1,024-lane work-group limit) on the
-    full-size Chung-Lu graph (1M rows, 9.1M nonzeros; H and C of 4-8 GB):
+    full-size Chung-Lu graph (1M rows, 9.1M nonzeros; H and C of 4-16 GB):
     all-ones features give exactly 1 (0 for empty rows) on rows no task
     splits and stay within the rounding bound on split rows; with seeded
-    features, sampled rows (random and the 200 highest-degree) match the
-    fp64 closed form.  Checked on the device, without copying C back."""
+    features the whole of C matches the reference-order oracle
+    (parallelMatrix.cpp:148-236) at 1e-5 relative / 1e-6 absolute, checked
+    in blocks of 1,024 feature columns."""
     torch = torch_mod()
     g = workloads.graph(2)
     S = workloads.candidate_s(g.nnz, 256)[2]
@@ -296,25 +315,14 @@ def test_full_chunglu_large_k_properties(gpu_ctx, K):
     bound = torch.from_numpy(((touch + 1) * 2.0**-23).astype(np.float32)).cuda()
     sp = torch.from_numpy(split).cuda()
     assert bool(((C[sp] - 1.0).abs() <= bound[sp, None]).all().item())
+    del whole, sp
     H = torch.empty((g.n, K), dtype=torch.float32, device="cuda")
     gpu_ctx.fill_features(H, g.n, K, workloads.FEATURE_SEED)
     C.fill_(float("nan"))
     t = gpu_ctx.spmm(d_rp, d_ci, d_v, d_o, g.n, g.nnz, H, g.n, K, d_t, len(p.tasks), C,
                      large_k=True)
-    assert not torch.isnan(C).any().item()
-    rng = np.random.default_rng(K)
-    rows = np.unique(np.concatenate([rng.integers(0, g.n, 300),
-                                     np.argsort(deg, kind="stable")[-200:]]))
-    got = C[torch.from_numpy(rows).cuda()].cpu().numpy()
-    for i, r in enumerate(rows):
-        lo, hi = g.row_ptr[r], g.row_ptr[r + 1]
-        exp = np.zeros(K)
-        if hi > lo:
-            cols = torch.from_numpy(g.col_idx[lo:hi].astype(np.int64)).cuda()
-            feats = H[cols].cpu().numpy().astype(np.float64)
-            exp = (g.val[lo:hi, None].astype(np.float64) * feats).sum(0) / (hi - lo)
-        np.testing.assert_allclose(got[i], exp, rtol=RTOL, atol=ATOL)
     print(f"K={K} total_us={t.total_us:.1f}", flush=True)
+    _whole_c_vs_oracle_in_column_blocks(torch, C, H, p, f"chunglu K={K} S={S}")
 
 
 # ------------------------------------------------------------------ edge cases
@@ -1035,14 +1043,18 @@ MB = 1 << 20
 # (segment-size candidate index, tasks per wave, feature slices, run order,
 # XCD placement, hot-set bytes, waves per SIMD, flags[, column phases]);
 # None = the schedule cwlb_ctx_tune_schedule picks, which is what bench.py
-# times.  The first R-MAT entry is the headline launch of the benchmark (64
-# tasks per wave, 2 feature slices, 48 MB cache hints, the standard kernel)
-# at every candidate S; the mesh entries are the launches its tuner kept
+# times (bench.py also checks the whole C of its own timed launch).  The
+# first R-MAT entries are headline launches of the benchmark (64 tasks per
+# wave, 2 feature slices, 48 MB cache hints, the standard kernel) at every
+# candidate S, and the launch a timed benchmark run kept at S = 125 (32 tasks
+# per wave, 2 slices, 48 MB hints, automatic placement); the mesh entries
+# are the launches its tuner kept
 # (runs by output row, contiguous XCD stretches, the occupancy variant); the
 # SBM's phased entries are its tuner's launch (12 phases, 8 slices) and the
 # best point of a phase sweep in task order (16 phases, 4 slices).
 FULL_LAUNCHES = {
     4: [(0, 64, 2, 1, 1, 48 * MB, 0, 0), (2, 64, 2, 1, 1, 48 * MB, 0, 0),
+        (2, 32, 2, 0, 0, 48 * MB, 0, 0), (2, None),
         (2, 64, 4, 1, 1, 0, 6, 0), (1, 64, 2, 1, 1, 48 * MB, 0, 0),
         (1, None), (1, 0, 0, 0, 0, 0, 0, 0), (1, 0, 0, 0, 0, 0, 0, capi.PER_TASK),
         (1, 4, 0, 2, 1, 0, 0, 0), (1, 8, 0, 2, 2, 0, 0, 0), (1, 32, 0, 1, 2, 0, 0, 0),
@@ -1123,6 +1135,54 @@ def test_full_size_launches_vs_oracle(gpu_ctx, cfg):
             gpu_ctx.set_cache_hints(0)
             gpu_ctx.set_occupancy(0)
             gpu_ctx.set_column_phases(0)
+    finally:
+        gpu_ctx.set_schedule(0, 0)
+        gpu_ctx.set_locality(0, 0)
+        gpu_ctx.set_cache_hints(0)
+        gpu_ctx.set_occupancy(0)
+        gpu_ctx.set_column_phases(0)
+
+
+MESH_S_SWEEP = (32, 64, 128, 256, 512)
+
+
+def test_full_mesh_segment_size_sweep_vs_oracle(gpu_ctx):
+    """The full mesh (16M rows, 40M nonzeros, K = 32) at every segment size
+    of the reference's range sweep (main.cpp:657-711), the S values its
+    benchmark times: with the automatic schedule and with the schedule
+    cwlb_ctx_tune_schedule keeps for that S (placement included), the whole
+    of C against the reference-order oracle (parallelMatrix.cpp:148-236) at
+    1e-5 relative / 1e-6 absolute."""
+    torch = torch_mod()
+    g = workloads.graph(5)
+    K = workloads.FEATURE_DIM[5]
+    costs = capi.read_costs(paths.COST_FILE)
+    H = torch.empty((g.n, K), dtype=torch.float32, device="cuda")
+    gpu_ctx.fill_features(H, g.n, K, workloads.FEATURE_SEED)
+    H_host = synth.features(g.n, K, workloads.FEATURE_SEED)
+    C = torch.empty((g.n, K), dtype=torch.float32, device="cuda")
+    try:
+        for S in MESH_S_SWEEP:
+            p = problem(g, costs, S)
+            ref_dev = torch.from_numpy(oracle.spmm_mean_f32_omp(
+                p.row_ptr, p.col_idx, p.val, p.origin, H_host, p.tasks)).cuda()
+            d = [dev(x) for x in (p.row_ptr, p.col_idx, p.val, p.origin)]
+            d_t = dev(np.ascontiguousarray(p.tasks, np.int32).reshape(-1))
+            args = (d[0], d[1], d[2], d[3], g.n, g.nnz, H, g.n, K, d_t, len(p.tasks), C)
+            for tuned in (False, True):
+                gpu_ctx.set_schedule(0, 0)
+                gpu_ctx.set_locality(0, 0)
+                gpu_ctx.set_cache_hints(0)
+                gpu_ctx.set_occupancy(0)
+                gpu_ctx.set_column_phases(0)
+                if tuned:
+                    gpu_ctx.tune_schedule(*args, trials=3, locality=True)
+                C.fill_(float("nan"))
+                gpu_ctx.spmm(*args)
+                what = f"mesh S={S} tasks={len(p.tasks)} tuned={tuned} ran={gpu_ctx.last_launch()}"
+                print(what, flush=True)
+                _assert_close_on_device(torch, C, ref_dev, what)
+            del ref_dev, d, d_t
     finally:
         gpu_ctx.set_schedule(0, 0)
         gpu_ctx.set_locality(0, 0)
