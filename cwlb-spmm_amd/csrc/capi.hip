@@ -48,6 +48,20 @@ cwlb_status check_spmm_args(cwlb_ctx* ctx, const SpmmArgs& a)
     return CWLB_OK;
 }
 
+// Entry points that allocate, read results back or synchronise cannot be
+// recorded into a graph: on a stream under capture they return
+// CWLB_UNSUPPORTED before enqueueing anything, so the capture stays valid.
+cwlb_status refuse_under_capture(hipStream_t st, const char* what)
+{
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    CWLB_HIP_TRY(hipStreamIsCapturing(st, &capture));
+    if (capture != hipStreamCaptureStatusNone)
+        return fail(CWLB_UNSUPPORTED, std::string(what) +
+                                          ": not available on a stream under graph capture "
+                                          "(it allocates and synchronises)");
+    return CWLB_OK;
+}
+
 // Reads the status word the last aggregation left (the stream must be idle).
 cwlb_status read_status(cwlb_ctx* ctx)
 {
@@ -294,6 +308,7 @@ cwlb_status cwlb_ctx_create(int device, void* stream, cwlb_ctx** out)
     hipError_t e = hipSuccess;
     for (auto& ev : c->ev)
         if (e == hipSuccess) e = hipEventCreate(&ev);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&c->switch_ev, hipEventDisableTiming);
     if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&c->d_status), 2 * sizeof(int));
     if (e == hipSuccess) e = hipMemset(c->d_status, 0, 2 * sizeof(int));
     if (e != hipSuccess) {
@@ -310,6 +325,7 @@ cwlb_status cwlb_ctx_destroy(cwlb_ctx* ctx)
     DeviceGuard g(ctx->device);
     for (auto& ev : ctx->ev)
         if (ev) (void)hipEventDestroy(ev);
+    if (ctx->switch_ev) (void)hipEventDestroy(ctx->switch_ev);
     if (ctx->d_status) (void)hipFree(ctx->d_status);
     for (void* p : {static_cast<void*>(ctx->d_run_keys), static_cast<void*>(ctx->d_run_keys_sorted),
                     static_cast<void*>(ctx->d_run_order), ctx->d_sort_temp,
@@ -330,7 +346,28 @@ cwlb_status cwlb_ctx_destroy(cwlb_ctx* ctx)
 cwlb_status cwlb_ctx_set_stream(cwlb_ctx* ctx, void* stream)
 {
     if (!ctx) return fail(CWLB_INVALID_ARG, "null context");
-    ctx->stream = static_cast<hipStream_t>(stream);
+    const auto next = static_cast<hipStream_t>(stream);
+    if (next != ctx->stream) {
+        // Calls on the old stream may still read or rewrite the context's
+        // own buffers (status words, column-phase bounds, the band-sorted
+        // copy); the new stream waits for everything enqueued on the old
+        // one so far, so a call on it cannot overwrite them under a call
+        // still running there.  Skipped when either stream is under graph
+        // capture: a wait on a captured event would pull the other stream
+        // into the capture (ordering against a graph is the caller's).
+        DeviceGuard g(ctx->device);
+        hipStreamCaptureStatus old_cap = hipStreamCaptureStatusNone;
+        hipStreamCaptureStatus new_cap = hipStreamCaptureStatusNone;
+        const bool known = hipStreamIsCapturing(ctx->stream, &old_cap) == hipSuccess &&
+                           hipStreamIsCapturing(next, &new_cap) == hipSuccess;
+        (void)hipGetLastError();  // a refused query (legacy stream during a capture) is not kept
+        if (known && old_cap == hipStreamCaptureStatusNone &&
+            new_cap == hipStreamCaptureStatusNone) {
+            CWLB_HIP_TRY(hipEventRecord(ctx->switch_ev, ctx->stream));
+            CWLB_HIP_TRY(hipStreamWaitEvent(next, ctx->switch_ev, 0));
+        }
+    }
+    ctx->stream = next;
     return CWLB_OK;
 }
 
@@ -487,6 +524,11 @@ cwlb_status cwlb_ctx_tune_schedule(cwlb_ctx* ctx, const int32_t* row_ptr, const 
     SpmmArgs a{row_ptr, col_idx, val, origin, n_rows, nnz, H, h_rows, K, tasks, n_tasks, C};
     cwlb_status st = check_spmm_args(ctx, a);
     if (st != CWLB_OK) return st;
+    {
+        DeviceGuard g(ctx->device);
+        st = refuse_under_capture(ctx->stream, "cwlb_ctx_tune_schedule");
+        if (st != CWLB_OK) return st;
+    }
     // Candidates: the automatic choice, then every run length and slice
     // count the kernel takes for this K.
     std::vector<std::pair<int, int>> cands{{0, 0}};
@@ -751,6 +793,8 @@ cwlb_status cwlb_spmm_mean_f32_host(cwlb_ctx* ctx, const int32_t* row_ptr,
         return fail(CWLB_INVALID_ARG, "spmm: negative size");
     if (nnz > INT32_MAX) return fail(CWLB_INVALID_ARG, "spmm: nnz must fit int32");
     DeviceGuard g(ctx->device);
+    const cwlb_status cs = refuse_under_capture(ctx->stream, "cwlb_spmm_mean_f32_host");
+    if (cs != CWLB_OK) return cs;
     const size_t out_elems = static_cast<size_t>(n_rows) * static_cast<size_t>(K);
     if (K == 0 || n_tasks == 0) {
         if (out_elems) std::memset(C, 0, out_elems * sizeof(float));
@@ -827,6 +871,8 @@ cwlb_status cwlb_reorder_by_degree_device(cwlb_ctx* ctx, int32_t n_rows, int64_t
     if (n_rows < 0 || nnz < 0 || nnz > INT32_MAX)
         return fail(CWLB_INVALID_ARG, "reorder: bad sizes");
     DeviceGuard g(ctx->device);
+    const cwlb_status cs = refuse_under_capture(ctx->stream, "cwlb_reorder_by_degree_device");
+    if (cs != CWLB_OK) return cs;
     return launch_reorder(ctx, n_rows, nnz, row_ptr, col_idx, val, origin, row_ptr_out,
                           col_idx_out, val_out);
 }
@@ -839,6 +885,8 @@ cwlb_status cwlb_partition_device(cwlb_ctx* ctx, const int32_t* row_ptr, int32_t
     if (n_rows > 0 && !row_ptr) return fail(CWLB_INVALID_ARG, "cwlb_partition_device: null row_ptr");
     if (capacity_tasks < 0) return fail(CWLB_INVALID_ARG, "cwlb_partition_device: negative capacity");
     DeviceGuard g(ctx->device);
+    const cwlb_status cs = refuse_under_capture(ctx->stream, "cwlb_partition_device");
+    if (cs != CWLB_OK) return cs;
     return launch_partition(ctx, row_ptr, n_rows, costs, capacity_weight, out, capacity_tasks,
                             n_tasks);
 }
@@ -851,6 +899,8 @@ cwlb_status cwlb_calibrate_report(cwlb_ctx* ctx, int32_t K, int32_t repeat, int3
     if (K <= 0 || repeat <= 0 || WI <= 0 || load_MB <= 0 || atomic_writers <= 0)
         return fail(CWLB_INVALID_ARG, "All microbenchmark parameters must be positive.");
     DeviceGuard g(ctx->device);
+    const cwlb_status cs = refuse_under_capture(ctx->stream, "cwlb_calibrate");
+    if (cs != CWLB_OK) return cs;
     return run_calibration(ctx, K, repeat, WI, load_MB, atomic_writers, out, report);
 }
 

@@ -79,8 +79,11 @@ constexpr int kBatch = 8;
 __global__ void __launch_bounds__(kBlock)
 band_sort(const int* __restrict__ rp, const int* __restrict__ ci, const float* __restrict__ val,
           int n_rows, long long nnz, long long h_rows, int P, int* __restrict__ bounds,
-          int* __restrict__ ci_out, float* __restrict__ val_out)
+          int* __restrict__ ci_out, float* __restrict__ val_out, int* __restrict__ chain_word)
 {
+    // The aggregation's not-a-chain word starts each phased call cleared
+    // (the clearing pass that runs next sets it for a list that is no chain).
+    if (chain_word && blockIdx.x == 0 && threadIdx.x == 0) *chain_word = 0;
     __shared__ int s_col[kWavesPerBlock][64 * kBatch];
     __shared__ float s_val[kWavesPerBlock][64 * kBatch];
     const int lane = threadIdx.x & 63;
@@ -218,12 +221,13 @@ cwlb_status grow(cwlb_ctx* ctx, T** p, long long* cap, long long want)
 
 cwlb_status launch_band_sort(hipStream_t st, const int32_t* row_ptr, const int32_t* col_idx,
                              const float* val, int32_t n_rows, int64_t nnz, int64_t h_rows,
-                             int phases, int32_t* bounds, int32_t* col_out, float* val_out)
+                             int phases, int32_t* bounds, int32_t* col_out, float* val_out,
+                             int32_t* chain_word)
 {
     if (n_rows <= 0 || phases < 2) return CWLB_OK;
     hipLaunchKernelGGL(band_sort, dim3(band_grid(n_rows)), dim3(kBlock), 0, st, row_ptr, col_idx,
                        val, n_rows, static_cast<long long>(nnz), static_cast<long long>(h_rows),
-                       phases, bounds, col_out, val_out);
+                       phases, bounds, col_out, val_out, chain_word);
     CWLB_LAUNCH_CHECK("band_sort");
     return CWLB_OK;
 }

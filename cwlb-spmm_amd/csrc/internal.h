@@ -13,6 +13,9 @@ struct cwlb_ctx {
     int device = 0;
     hipStream_t stream = nullptr;
     hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
+    // Recorded on the old stream by cwlb_ctx_set_stream for the new one to
+    // wait on.
+    hipEvent_t switch_ev = nullptr;
     int compute_units = 0;
     int max_wg = 0;
     int wave = 64;
@@ -23,8 +26,8 @@ struct cwlb_ctx {
     // Device status words written by the kernels.  [0]: bit 0 = a column
     // index was outside [0, h_rows), bit 1 = an origin entry was outside
     // [0, n_rows), bit 2 = a row's offsets left [0, nnz] or decreased.
-    // [1]: the sequence number of the last column-phased call whose task
-    // list was not a chain.
+    // [1]: cleared by each column-phased call's band sort, then set to the
+    // call's sequence number when its task list is not a chain.
     int* d_status = nullptr;
     // Schedule overrides (0 = automatic): tasks per wave, feature slices,
     // run order (1 = task order, 2 = by output row id) and block placement
@@ -193,10 +196,12 @@ cwlb_status prepare_column_phases(cwlb_ctx* ctx, const SpmmArgs& a, int phases, 
 
 // Enqueues the band sort: bounds[(p - 1) * n_rows + r] for p in [1, phases)
 // (bounds may be null) and, when col_out is non-null, the band-sorted copy
-// of col_idx and val.
+// of col_idx and val.  A non-null chain_word (the aggregation's status[1])
+// is cleared by the same launch.
 cwlb_status launch_band_sort(hipStream_t st, const int32_t* row_ptr, const int32_t* col_idx,
                              const float* val, int32_t n_rows, int64_t nnz, int64_t h_rows,
-                             int phases, int32_t* bounds, int32_t* col_out, float* val_out);
+                             int phases, int32_t* bounds, int32_t* col_out, float* val_out,
+                             int32_t* chain_word = nullptr);
 
 cwlb_status launch_reorder(cwlb_ctx* ctx, int32_t n_rows, int64_t nnz, const int32_t* row_ptr,
                            const int32_t* col_idx, const float* val, int32_t* origin,

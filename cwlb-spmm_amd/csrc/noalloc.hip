@@ -100,6 +100,16 @@ extern "C" cwlb_status cwlb_spmm_mean_f32_noalloc(
             return fail(CWLB_INVALID_ARG, "spmm: null device pointer");
     }
     if (n_rows > 0 && K > 0 && !C) return fail(CWLB_INVALID_ARG, "spmm: null C");
+    if (synchronize) {
+        // The status read-back and the wait cannot be recorded into a graph;
+        // refused before anything is enqueued, so the capture stays valid.
+        hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+        CWLB_HIP_TRY(hipStreamIsCapturing(static_cast<hipStream_t>(stream), &capture));
+        if (capture != hipStreamCaptureStatusNone)
+            return fail(CWLB_INVALID_ARG,
+                        "cwlb_spmm_mean_f32_noalloc: synchronize must be 0 on a stream under "
+                        "graph capture");
+    }
 
     // A context on the stack: default schedule or the given run length and
     // slices, task order, no cache hints.  Nothing in it is allocated (its

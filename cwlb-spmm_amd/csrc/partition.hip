@@ -181,6 +181,15 @@ cwlb_status exclusive_scan(hipStream_t st, In in, Out out, size_t n)
 
 unsigned grid_for(long long n) { return static_cast<unsigned>((n + kBlock - 1) / kBlock); }
 
+// Clears one or two words with a kernel rather than hipMemsetAsync (memset
+// nodes are kept out of anything a caller may record into a graph).
+template <class T>
+__global__ void part_clear(T* __restrict__ a, T* __restrict__ b)
+{
+    *a = T(0);
+    if (b) *b = T(0);
+}
+
 }  // namespace
 
 cwlb_status launch_partition(cwlb_ctx* ctx, const int32_t* rp, int32_t n,
@@ -221,8 +230,9 @@ cwlb_status launch_partition(cwlb_ctx* ctx, const int32_t* rp, int32_t n,
     CWLB_HIP_TRY(scan.alloc(sizeof(int) * (n + 1)));
     CWLB_HIP_TRY(long_idx.alloc(sizeof(int) * n));
     CWLB_HIP_TRY(status.alloc(sizeof(int)));
-    CWLB_HIP_TRY(hipMemsetAsync(status.p, 0, sizeof(int), st));
-    CWLB_HIP_TRY(hipMemsetAsync(is_long.as<int>() + n, 0, sizeof(int), st));
+    hipLaunchKernelGGL(part_clear<int>, dim3(1), dim3(1), 0, st, status.as<int>(),
+                       is_long.as<int>() + n);
+    CWLB_LAUNCH_CHECK("part_clear");
     hipLaunchKernelGGL(part_flags, dim3(grid_for(n)), dim3(kBlock), 0, st, p, is_long.as<int>());
     CWLB_LAUNCH_CHECK("part_flags");
     cwlb_status s = exclusive_scan(st, is_long.as<int>(), scan.as<int>(), static_cast<size_t>(n) + 1);
@@ -273,7 +283,9 @@ cwlb_status launch_partition(cwlb_ctx* ctx, const int32_t* rp, int32_t n,
     const long long len = 1LL << (levels - 1);
     Mem chain, counts, offsets;
     CWLB_HIP_TRY(chain.alloc(sizeof(int) * len));
-    CWLB_HIP_TRY(hipMemsetAsync(chain.p, 0, sizeof(int), st));
+    hipLaunchKernelGGL(part_clear<int>, dim3(1), dim3(1), 0, st, chain.as<int>(),
+                       static_cast<int*>(nullptr));
+    CWLB_LAUNCH_CHECK("part_clear");
     // 3. expansion: positions that are multiples of 2 * half get their
     // successor half steps on.
     for (int j = levels - 2; j >= 0; --j) {
@@ -286,7 +298,9 @@ cwlb_status launch_partition(cwlb_ctx* ctx, const int32_t* rp, int32_t n,
     // 4. task offsets of the chain nodes.
     CWLB_HIP_TRY(counts.alloc(sizeof(long long) * (len + 1)));
     CWLB_HIP_TRY(offsets.alloc(sizeof(long long) * (len + 1)));
-    CWLB_HIP_TRY(hipMemsetAsync(counts.as<long long>() + len, 0, sizeof(long long), st));
+    hipLaunchKernelGGL(part_clear<long long>, dim3(1), dim3(1), 0, st,
+                       counts.as<long long>() + len, static_cast<long long*>(nullptr));
+    CWLB_LAUNCH_CHECK("part_clear");
     hipLaunchKernelGGL(part_chain_counts, dim3(grid_for(len)), dim3(kBlock), 0, st, len, n,
                        chain.as<int>(), cnt.as<int>(), counts.as<long long>());
     CWLB_LAUNCH_CHECK("part_chain_counts");

@@ -160,6 +160,15 @@ gather_long(const int* __restrict__ rp, const int* __restrict__ ci, const float*
 
 __global__ void set_first_zero(int* __restrict__ p) { p[0] = 0; }
 
+// The two status words of the reorder, cleared by a kernel rather than
+// hipMemsetAsync (memset nodes are kept out of anything a caller may record
+// into a graph).
+__global__ void clear_two(int* __restrict__ p)
+{
+    p[0] = 0;
+    p[1] = 0;
+}
+
 struct DevMem {
     void* p = nullptr;
     DevMem() = default;
@@ -299,7 +308,8 @@ cwlb_status launch_reorder(cwlb_ctx* ctx, int32_t n, int64_t nnz, const int32_t*
     auto* d_sorted = static_cast<unsigned*>(keys_sorted.p);
     auto* d_status = static_cast<int*>(flags.p);
     auto* d_max = reinterpret_cast<unsigned*>(d_status + 1);
-    CWLB_HIP_TRY(hipMemsetAsync(d_status, 0, 2 * sizeof(int), st));
+    hipLaunchKernelGGL(clear_two, dim3(1), dim3(1), 0, st, d_status);
+    CWLB_LAUNCH_CHECK("clear_two");
     hipLaunchKernelGGL(degree_keys, dim3(grid), dim3(kBlock), 0, st, rp, n,
                        static_cast<long long>(nnz), d_keys, d_status,
                        static_cast<unsigned*>(bmax.p));

@@ -855,8 +855,8 @@ spmm_mean_runs(const int* __restrict__ rp, const int* __restrict__ ci,
 // the pass also checks that the list is a chain -- every task well formed
 // and continuing its predecessor, so that no two tasks share a nonzero and
 // a row covered whole by one segment is touched by no other -- and
-// otherwise writes seq into status[1] (which nothing resets: a stale value
-// differs from every later call's seq).
+// otherwise writes seq into status[1] (the call's band sort, which runs
+// just before, cleared it; seq is never 0).
 template <int VEC>
 __global__ void __launch_bounds__(kAuxBlock)
 zero_split_rows(const int* __restrict__ rp, const int* __restrict__ origin, int n_rows,

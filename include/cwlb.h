@@ -96,6 +96,11 @@ const char* cwlb_last_error(void);
  * sycl::queue the reference passes around (main.cpp:514-516). */
 cwlb_status cwlb_ctx_create(int device, void* stream, cwlb_ctx** out);
 cwlb_status cwlb_ctx_destroy(cwlb_ctx* ctx);
+/* Later calls run on `stream`.  The new stream first waits for all work
+ * enqueued on the old one so far (an event recorded there), because calls
+ * still running on the old stream may read the context's own buffers that a
+ * call on the new one rewrites.  Not done when either stream is under graph
+ * capture: ordering against a captured graph is then the caller's. */
 cwlb_status cwlb_ctx_set_stream(cwlb_ctx* ctx, void* stream);
 /* Waits for the context's stream; then reports, as CWLB_INVALID_ARG, a bad
  * column index, origin entry or row offset that the last aggregation met
@@ -180,7 +185,9 @@ cwlb_status cwlb_ctx_get_occupancy(cwlb_ctx* ctx, int32_t* waves_per_simd);
  * freed before cwlb_ctx_destroy.  Applies to task lists that are chains -- every task
  * well formed and starting where its predecessor ended, as
  * cwlb_partition's lists are -- which the device checks on every call; any
- * other list runs in one pass (over the band-sorted copy).  Applies with
+ * other list runs in one pass over the caller's col_idx and val (its task
+ * offsets index them), and the band sort it already paid for is unused.
+ * Applies with
  * 16-byte aligned H and C, K a multiple of 4 and at most 256 floats per
  * feature slice, without CWLB_SPMM_PER_TASK; replaces the occupancy variant
  * and the cache hints while on.  Results agree with the one-pass ones

@@ -407,38 +407,113 @@ def test_tuner_tries_phases(gpu_ctx, reset):
     torch.cuda.empty_cache()
 
 
-def test_stream_switch_after_builds(gpu_ctx, reset):
-    """The run order and the phase bounds built by an asynchronous call on
-    one stream serve a call on another stream right after (the building
-    call synchronises its stream)."""
+def test_stream_switch_orders_the_streams(gpu_ctx, reset):
+    """An asynchronous phased call on stream A, then cwlb_ctx_set_stream(B)
+    and a phased call on other arrays (another graph, task list and feature
+    width): B's band sort rewrites the context's band-sorted copy and row
+    bounds that A's phases read, so B must start after A's work.  Both
+    results match the oracle; then back on A, a third call on A's arrays
+    (after B's) does too.  Run order and XCD placement as built by the
+    calls."""
     torch = torch_mod()
-    g = workloads.small(4, seed=12)
-    K = 64
-    p = problem(g, SKEWED_COSTS, 7)
-    d_rp, d_ci, d_v, d_o = dev(p.row_ptr), dev(p.col_idx), dev(p.val), dev(p.origin)
-    d_t = dev(np.ascontiguousarray(p.tasks).reshape(-1))
-    H = synth.features(g.n, K, 8)
-    d_H = dev(H)
-    ref = oracle.spmm_mean_f32(p.row_ptr, p.col_idx, p.val, p.origin, H, p.tasks)
+    probs = []
+    for cfg, seed, K, S in ((4, 12, 256, 7), (1, 13, 64, 5)):
+        g = workloads.small(cfg, seed=seed)
+        p = problem(g, SKEWED_COSTS, S)
+        H = synth.features(g.n, K, seed)
+        d = [dev(x) for x in (p.row_ptr, p.col_idx, p.val, p.origin)]
+        d_t = dev(np.ascontiguousarray(p.tasks).reshape(-1))
+        ref = oracle.spmm_mean_f32(p.row_ptr, p.col_idx, p.val, p.origin, H, p.tasks)
+        probs.append((g, p, K, d, d_t, dev(H), ref))
     a, b = torch.cuda.Stream(), torch.cuda.Stream()
-    Ca = torch.zeros((g.n, K), dtype=torch.float32, device="cuda")
-    Cb = torch.zeros_like(Ca)
+    Cs = [torch.full((pr[0].n, pr[2]), float("nan"), dtype=torch.float32, device="cuda")
+          for pr in probs]
     torch.cuda.synchronize()
     set_phased(gpu_ctx, 7, 4, 2, order=2, xcd=2)
+
+    def call(i):
+        g, p, K, d, d_t, d_H, _ = probs[i]
+        gpu_ctx.spmm(d[0], d[1], d[2], d[3], g.n, g.nnz, d_H, g.n, K, d_t, len(p.tasks), Cs[i],
+                     timed=False)
+        return gpu_ctx.last_launch()
+
     try:
         gpu_ctx.set_stream(a.cuda_stream)
-        gpu_ctx.spmm(d_rp, d_ci, d_v, d_o, g.n, g.nnz, d_H, g.n, K, d_t, len(p.tasks), Ca,
-                     timed=False)
+        info_a = call(0)
         gpu_ctx.set_stream(b.cuda_stream)
-        gpu_ctx.spmm(d_rp, d_ci, d_v, d_o, g.n, g.nnz, d_H, g.n, K, d_t, len(p.tasks), Cb,
-                     timed=False)
-        info = gpu_ctx.last_launch()
+        info_b = call(1)
         torch.cuda.synchronize()
+        got = [C.cpu().numpy() for C in Cs]
+        Cs[0].fill_(float("nan"))
+        torch.cuda.synchronize()
+        gpu_ctx.set_stream(a.cuda_stream)
+        call(0)
+        torch.cuda.synchronize()
+        again = Cs[0].cpu().numpy()
     finally:
         gpu_ctx.set_stream(torch.cuda.current_stream().cuda_stream)
-    assert (info["column_phases"], info["run_order"]) == (7, 2), info
-    check(Ca.cpu().numpy(), ref)
-    check(Cb.cpu().numpy(), ref)
+    assert info_a["column_phases"] == 7 and info_b["column_phases"] == 7, (info_a, info_b)
+    check(got[0], probs[0][6])
+    check(got[1], probs[1][6])
+    check(again, probs[0][6])
+
+
+def test_chain_check_resets_between_graph_replays(gpu_ctx):
+    """A phased call captured into a graph, replayed over a chain, then over
+    a list that is not a chain (the same tasks shuffled, written into the
+    captured task array), then over the chain again: the last replay runs
+    phased again (its C is bit-identical to the first replay's, and differs
+    from the one-pass result, which rounds differently), and every replay
+    matches the oracle.  One run of all tasks per wave (tasks_per_wave
+    2^20) keeps every result deterministic."""
+    torch = torch_mod()
+    g = workloads.small(1, seed=17)
+    K = 64
+    p = problem(g, SKEWED_COSTS, 6)
+    H_host = synth.features(g.n, K, 17)
+    d_rp, d_ci, d_v, d_o = dev(p.row_ptr), dev(p.col_idx), dev(p.val), dev(p.origin)
+    chain = np.ascontiguousarray(p.tasks, np.int32)
+    shuffled = np.ascontiguousarray(chain[np.random.default_rng(3).permutation(len(chain))])
+    d_t = dev(chain.reshape(-1))
+    H = dev(H_host)
+    C = torch.zeros((g.n, K), dtype=torch.float32, device="cuda")
+    args = (d_rp, d_ci, d_v, d_o, g.n, g.nnz, H, g.n, K, d_t, len(chain), C)
+    ctx = capi.Context(0, torch.cuda.current_stream().cuda_stream)
+    try:
+        set_phased(ctx, 4, 1 << 20, 1)
+        ctx.spmm(*args, flags=capi.ZERO_OUTPUT)  # sizes the phase buffers
+        phased_eager = C.cpu().numpy()
+        ctx.set_column_phases(0)
+        ctx.spmm(*args, flags=capi.ZERO_OUTPUT)
+        one_pass = C.cpu().numpy()
+        ctx.set_column_phases(4)
+        graph = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            ctx.set_stream(side.cuda_stream)
+            with torch.cuda.graph(graph, stream=side):
+                ctx.spmm(*args, flags=capi.ZERO_OUTPUT, timed=False)
+        ctx.set_stream(torch.cuda.current_stream().cuda_stream)
+        assert ctx.last_launch()["column_phases"] == 4
+        torch.cuda.synchronize()
+        got = []
+        for tasks in (chain, shuffled, chain):
+            d_t.copy_(torch.from_numpy(tasks.reshape(-1)))
+            C.fill_(float("nan"))
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            got.append(C.cpu().numpy())
+        del graph
+    finally:
+        ctx.close()
+    ref = oracle.spmm_mean_f32(p.row_ptr, p.col_idx, p.val, p.origin, H_host, chain)
+    for c in got:
+        check(c, ref)
+    assert not np.array_equal(phased_eager, one_pass)  # the two paths are told apart
+    assert np.array_equal(got[0], phased_eager)
+    assert np.array_equal(got[2], got[0])
 
 
 @pytest.mark.parametrize("P", [3, 16])

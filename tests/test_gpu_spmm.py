@@ -1352,6 +1352,75 @@ def test_graph_replay_after_rebuild_on_other_arrays(gpu_ctx):
         gpu_ctx.set_cache_hints(0)
 
 
+def test_allocating_entries_refused_under_capture(gpu_ctx):
+    """The entry points that allocate, read back or synchronise -- the GPU
+    reorder and partition, the host-pointer call, the calibration and the
+    schedule tuner -- return CWLB_UNSUPPORTED on a stream under graph
+    capture before enqueueing anything: the capture stays valid, and an
+    aggregation call captured after them replays to the oracle's result
+    (with eager work between replays)."""
+    torch = torch_mod()
+    g = workloads.small(4, seed=41)
+    K = 64
+    p = problem(g, SKEWED_COSTS, 8)
+    H_host = synth.features(g.n, K, 6)
+    d_rp0, d_ci0, d_v0 = dev(g.row_ptr), dev(g.col_idx), dev(g.val)
+    d_rp, d_ci, d_v, d_o = dev(p.row_ptr), dev(p.col_idx), dev(p.val), dev(p.origin)
+    d_t = dev(np.ascontiguousarray(p.tasks, np.int32).reshape(-1))
+    H = dev(H_host)
+    C = torch.zeros((g.n, K), dtype=torch.float32, device="cuda")
+    outs = [torch.zeros(g.n, dtype=torch.int32, device="cuda"),
+            torch.zeros(g.n + 1, dtype=torch.int32, device="cuda"),
+            torch.zeros(g.nnz, dtype=torch.int32, device="cuda"),
+            torch.zeros(g.nnz, dtype=torch.float32, device="cuda")]
+    t_out = torch.zeros((len(p.tasks), 4), dtype=torch.int32, device="cuda")
+    args = (d_rp, d_ci, d_v, d_o, g.n, g.nnz, H, g.n, K, d_t, len(p.tasks), C)
+    refused = {
+        "reorder": lambda: gpu_ctx.reorder_device(g.n, g.nnz, d_rp0, d_ci0, d_v0, *outs),
+        "partition": lambda: gpu_ctx.partition_device(d_rp, g.n, SKEWED_COSTS, p.capacity, t_out,
+                                                      len(p.tasks)),
+        "host_call": lambda: gpu_ctx.spmm_host(p.row_ptr, p.col_idx, p.val, p.origin, H_host,
+                                               p.tasks),
+        "calibrate": lambda: gpu_ctx.calibrate(K=32, repeat=2, WI=4096, load_MB=8),
+        "tune": lambda: gpu_ctx.tune_schedule(*args, trials=1),
+    }
+    statuses = {}
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    try:
+        with torch.cuda.stream(side):
+            gpu_ctx.set_stream(side.cuda_stream)
+            with torch.cuda.graph(graph, stream=side):
+                for name, fn in refused.items():
+                    try:
+                        fn()
+                        statuses[name] = (capi.OK, "")
+                    except capi.CwlbError as e:
+                        statuses[name] = (e.status, str(e))
+                gpu_ctx.spmm(*args, timed=False)
+    finally:
+        gpu_ctx.set_stream(torch.cuda.current_stream().cuda_stream)
+    for name, (status, msg) in statuses.items():
+        assert status == capi.UNSUPPORTED and "graph capture" in msg, (name, status, msg)
+    torch.cuda.synchronize()
+    ref = oracle.spmm_mean_f32(p.row_ptr, p.col_idx, p.val, p.origin, H_host, p.tasks)
+    for i in range(3):
+        C.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        check(C.cpu().numpy(), ref)
+        _ = (H * 2.0).sum().item()  # eager work between replays
+    # Outside capture the same entries run: the reorder and partition match
+    # the host's.
+    gpu_ctx.reorder_device(g.n, g.nnz, d_rp0, d_ci0, d_v0, *outs)
+    assert np.array_equal(outs[1].cpu().numpy(), p.row_ptr)
+    n_t = gpu_ctx.partition_device(d_rp, g.n, SKEWED_COSTS, p.capacity, t_out, len(p.tasks))
+    assert n_t == len(p.tasks) and np.array_equal(t_out.cpu().numpy(), p.tasks)
+
+
 def test_tune_schedule(gpu_ctx):
     """cwlb_ctx_tune_schedule picks one of its candidates, leaves it on the
     context, and every schedule it tried computes the same result.  A hot

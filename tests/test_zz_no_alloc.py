@@ -120,3 +120,35 @@ def test_noalloc_captured_into_a_graph(gpu_ctx):
         torch.cuda.synchronize()
         np.testing.assert_allclose(C.cpu().numpy(), want, rtol=RTOL, atol=ATOL)
         _ = (d_H * 2.0).sum().item()  # eager work between replays
+
+
+def test_noalloc_synchronize_refused_under_capture(gpu_ctx):
+    """Under graph capture, a call that asks to synchronise (read the status
+    word back and wait) is refused with CWLB_INVALID_ARG before anything is
+    enqueued: the capture stays valid, and the call captured after it with
+    synchronize=False replays to the context entry's result."""
+    import torch
+    g, p, H, d, d_H, d_t = _inputs(torch, 4, 35, 64, 7, SKEWED_COSTS)
+    _, want = _both(gpu_ctx, torch, g, p, d, d_H, d_t, 64)
+    C = torch.zeros((g.n, 64), dtype=torch.float32, device="cuda")
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    status = None
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            try:
+                capi.spmm_noalloc(side.cuda_stream, d[0], d[1], d[2], d[3], g.n, g.nnz, d_H,
+                                  g.n, 64, d_t, len(p.tasks), C, synchronize=True)
+            except capi.CwlbError as e:
+                status, msg = e.status, str(e)
+            capi.spmm_noalloc(side.cuda_stream, d[0], d[1], d[2], d[3], g.n, g.nnz, d_H, g.n,
+                              64, d_t, len(p.tasks), C, synchronize=False)
+    assert status == capi.INVALID_ARG and "graph capture" in msg
+    torch.cuda.synchronize()
+    for _ in range(2):
+        C.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        np.testing.assert_allclose(C.cpu().numpy(), want, rtol=RTOL, atol=ATOL)
