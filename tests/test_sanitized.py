@@ -164,3 +164,53 @@ def test_search_grid_fuzz(lo, hi, third, mode):
         return
     fn = oracle.candidate_search_by_count if mode == "count" else oracle.candidate_search_by_step
     assert got == fn(lo, hi, third)
+
+
+# ---------------------------------------------------------------- ThreadSanitizer
+TSAN = os.path.join(HERE, "cxx", "bin", "dropin_probe_tsan")
+TSAN_ENV = dict(os.environ, TSAN_OPTIONS="halt_on_error=1:exitcode=66:report_signal_unsafe=0")
+
+
+def tsan(*args):
+    if not os.path.exists(TSAN):
+        pytest.fail(f"{TSAN} missing: build with __graft_entry__.build()")
+    r = subprocess.run([TSAN, *map(str, args)], capture_output=True, text=True, env=TSAN_ENV,
+                       timeout=600)
+    assert "ThreadSanitizer" not in r.stderr, r.stderr[-4000:]
+    assert r.returncode == 0, (r.returncode, r.stderr[-3000:])
+    return r.stdout
+
+
+@pytest.mark.parametrize("shape", ["rmat", "hub"])
+def test_threaded_reorder_under_tsan(tmp_path, shape):
+    """The host degree reordering (sortCSRByDegreeDPLCPU over
+    cwlb_reorder_by_degree: up to 16 threads over shared per-thread degree
+    histograms and row offsets) and the partition of its output, under
+    ThreadSanitizer, on a skewed R-MAT graph of 2^18 rows and about 4M
+    nonzeros (enough rows and nonzeros for every thread the host offers, up
+    to 16) and on one with a single hub row of 1M nonzeros: no race
+    reported, and the results are the oracle's."""
+    from cwlb_amd import synth
+    if shape == "rmat":
+        g = synth.rmat(18, 1 << 22, 0.57, 0.19, 0.19, 18)
+        rp, ci = g.row_ptr, g.col_idx
+    else:
+        n = 300_000
+        deg = np.ones(n, np.int64)
+        deg[12_345] = 1_000_000
+        rp = np.concatenate([[0], np.cumsum(deg)]).astype(np.int32)
+        ci = np.random.default_rng(5).integers(0, n, rp[-1]).astype(np.int32)
+    val = (np.arange(len(ci)) % 7 + 1).astype(np.float32)
+    write_csr(tmp_path / "in", rp, ci, val)
+    tsan("reorder-cpu", tmp_path / "in", tmp_path / "out")
+    from dropin_util import read_order
+    got = read_order(tmp_path / "out")
+    exp = oracle.reorder_by_degree(rp, ci, val)
+    for a, b in zip(got, exp):
+        assert np.array_equal(a, b)
+    costs = (0.125, 1.375, 0.75, 3.5)
+    tsan("partition", tmp_path / "out", *costs, 40, tmp_path / "t")
+    raw = open(tmp_path / "t", "rb").read()
+    cap = float(np.frombuffer(raw[:8], np.float64)[0])
+    tasks = np.frombuffer(raw[8:], np.int32).reshape(-1, 4)
+    assert np.array_equal(tasks, oracle.partition(exp[1], costs, cap))
