@@ -99,7 +99,8 @@ def schedule_args(S, sched):
     return ["--s", str(S), "--tasks-per-wave", str(sched["tasks_per_wave"]),
             "--slices", str(sched["feature_slices"]), "--run-order", str(sched["run_order"]),
             "--xcd-blocks", str(sched["xcd_blocks"]), "--hot-mb", str(sched["hot_bytes"] >> 20),
-            "--occupancy", str(sched["occupancy"]), "--phases", str(sched.get("phases", 0))]
+            "--occupancy", str(sched["occupancy"]), "--phases", str(sched.get("phases", 0)),
+            "--tiling", str(sched.get("tiling", 0))]
 
 
 def read_counter_csv(path):
@@ -206,6 +207,7 @@ def pmc_child(args):
     ctx.set_cache_hints(args.hot_mb << 20)
     ctx.set_occupancy(args.occupancy)
     ctx.set_column_phases(args.phases)
+    ctx.set_lane_tiling(args.tiling)
     for _ in range(1 + args.steps):
         ctx.spmm(d[0], d[1], d[2], d[3], g.n, g.nnz, H, g.n, K, d[4], len(tasks), C,
                  flags=capi.KEEP_EMPTY_ROWS, large_k=large_k)
@@ -322,6 +324,7 @@ def segment_size_sweep(ctx, call, tune, dev, tasks_for, cfg, costs, S, trials):
     ctx.set_cache_hints(0)
     ctx.set_occupancy(0)
     ctx.set_column_phases(0)
+    ctx.set_lane_tiling(0)
     for _ in range(3):
         call(d_t, len(tk), False)
     auto_us = float(np.mean([call(d_t, len(tk), True).main_us for _ in range(trials)]))
@@ -333,7 +336,8 @@ def segment_size_sweep(ctx, call, tune, dev, tasks_for, cfg, costs, S, trials):
             "tuned_us": round(tuned_us, 1),
             "schedule": {"tasks_per_wave": m, "feature_slices": sl, "run_order": order,
                          "xcd_blocks": xcd, "hot_bytes": ctx.cache_hints(),
-                         "occupancy": ctx.occupancy(), "phases": ctx.column_phases()},
+                         "occupancy": ctx.occupancy(), "phases": ctx.column_phases(),
+                         "tiling": ctx.lane_tiling()},
             "tasks_match_reference_fixture": reference_partition_match(cfg, S, costs, tk)}
 
 
@@ -425,6 +429,9 @@ def parse_args():
                     help="fixed schedule: 6 = the 6-waves-per-SIMD kernel variant")
     ap.add_argument("--phases", type=int, default=0,
                     help="fixed schedule: column phases (cwlb_ctx_set_column_phases)")
+    ap.add_argument("--tiling", type=int, default=0, choices=(0, 1, 2),
+                    help="fixed schedule: lane tiling (cwlb_ctx_set_lane_tiling: 1 power-of-two "
+                         "slots, 2 packed slots)")
     ap.add_argument("--run-order", type=int, default=0,
                     help="fixed run order (cwlb_ctx_set_locality: 1 task order, 2 by output row)")
     ap.add_argument("--xcd-blocks", type=int, default=0,
@@ -510,7 +517,7 @@ def main():
     # is kept.  A fixed schedule (--tasks-per-wave etc.) or --no-tune ranks
     # the S by the automatic schedule instead.
     fixed = bool(args.tasks_per_wave or args.slices or args.run_order or args.xcd_blocks
-                 or args.hot_mb or args.occupancy or args.phases)
+                 or args.hot_mb or args.occupancy or args.phases or args.tiling)
     tuning = not fixed and not args.no_tune
     cands = [args.s] if args.s else workloads.candidate_s(g.nnz, info.compute_units)
     best = None
@@ -524,6 +531,7 @@ def main():
         ctx.set_cache_hints(0)
         ctx.set_occupancy(0)
         ctx.set_column_phases(0)
+        ctx.set_lane_tiling(0)
         for _ in range(5):
             call(d_t, len(tk), False)
         us = float(np.mean([call(d_t, len(tk), True).total_us for _ in range(10)]))
@@ -536,7 +544,8 @@ def main():
             t_tune += rec["tuning_ms"]
             rec["schedule"] = {"tasks_per_wave": m, "feature_slices": sl, "run_order": order,
                                "xcd_blocks": xcd, "hot_bytes": ctx.cache_hints(),
-                               "occupancy": ctx.occupancy(), "phases": ctx.column_phases()}
+                               "occupancy": ctx.occupancy(), "phases": ctx.column_phases(),
+                               "tiling": ctx.lane_tiling()}
             for _ in range(3):
                 call(d_t, len(tk), False)
             rank = float(np.mean([call(d_t, len(tk), True).total_us for _ in range(10)]))
@@ -552,13 +561,13 @@ def main():
     log(f"preprocessing: {prep}")
     # Launch schedule for this graph and S (0, 0 = the automatic choice).
     schedule = {"tasks_per_wave": 0, "feature_slices": 0, "run_order": 0, "xcd_blocks": 0,
-                "hot_bytes": 0, "occupancy": 0, "phases": 0, "tuned": False,
+                "hot_bytes": 0, "occupancy": 0, "phases": 0, "tiling": 0, "tuned": False,
                 "automatic_schedule_us": round(float(auto_us), 1)}
     if fixed:
         schedule.update(tasks_per_wave=args.tasks_per_wave, feature_slices=args.slices,
                         run_order=args.run_order, xcd_blocks=args.xcd_blocks,
                         hot_bytes=args.hot_mb << 20, occupancy=args.occupancy,
-                        phases=args.phases)
+                        phases=args.phases, tiling=args.tiling)
         log(f"fixed schedule: {schedule}")
     elif tuning:
         # One cwlb_ctx_tune_schedule call per S candidate (each candidate's
@@ -572,6 +581,7 @@ def main():
         c.set_cache_hints(sched["hot_bytes"])
         c.set_occupancy(sched["occupancy"])
         c.set_column_phases(sched["phases"])
+        c.set_lane_tiling(sched.get("tiling", 0))
 
     apply(ctx, schedule)
 

@@ -453,6 +453,22 @@ cwlb_status cwlb_ctx_get_occupancy(cwlb_ctx* ctx, int32_t* waves_per_simd)
     return CWLB_OK;
 }
 
+cwlb_status cwlb_ctx_set_lane_tiling(cwlb_ctx* ctx, int32_t tiling)
+{
+    if (!ctx) return fail(CWLB_INVALID_ARG, "null context");
+    if (tiling < 0 || tiling > 2)
+        return fail(CWLB_INVALID_ARG, "tiling must be 0 (automatic), 1 (power-of-two slots) or 2 (packed)");
+    ctx->sched_tiling = tiling;
+    return CWLB_OK;
+}
+
+cwlb_status cwlb_ctx_get_lane_tiling(cwlb_ctx* ctx, int32_t* tiling)
+{
+    if (!ctx || !tiling) return fail(CWLB_INVALID_ARG, "null argument");
+    *tiling = ctx->sched_tiling;
+    return CWLB_OK;
+}
+
 cwlb_status cwlb_ctx_set_column_phases(cwlb_ctx* ctx, int32_t phases)
 {
     if (!ctx) return fail(CWLB_INVALID_ARG, "null context");
@@ -541,10 +557,12 @@ cwlb_status cwlb_ctx_tune_schedule(cwlb_ctx* ctx, const int32_t* row_ptr, const 
     const long long keep_hot = ctx->sched_hot_bytes;
     const int keep_occ = ctx->sched_occupancy;
     const int keep_phases = ctx->sched_phases;
+    const int keep_tiling = ctx->sched_tiling;
     if (locality_out) {
         ctx->sched_hot_bytes = 0;
         ctx->sched_occupancy = 0;
         ctx->sched_phases = 0;
+        ctx->sched_tiling = 0;
     }
     float best_us = 0.0f;
     std::pair<int, int> best{0, 0};
@@ -586,6 +604,7 @@ cwlb_status cwlb_ctx_tune_schedule(cwlb_ctx* ctx, const int32_t* row_ptr, const 
         ctx->sched_hot_bytes = keep_hot;
         ctx->sched_occupancy = keep_occ;
         ctx->sched_phases = keep_phases;
+        ctx->sched_tiling = keep_tiling;
     };
     const int keep_order = ctx->sched_order, keep_xcd = ctx->sched_xcd;
     for (const auto& c : cands) {
@@ -706,6 +725,17 @@ cwlb_status cwlb_ctx_tune_schedule(cwlb_ctx* ctx, const int32_t* row_ptr, const 
                 ctx->sched_tasks_per_wave = m6;
             }
         }
+        // Packed slots (cwlb_ctx_set_lane_tiling) under the settings so far,
+        // where they change the tiling; kept when faster, re-timed first.
+        if (st == CWLB_OK) {
+            st = time_current(&base, nullptr, 0.0f);
+            ctx->sched_tiling = 2;
+            float med = 0.0f;
+            if (st == CWLB_OK)
+                st = time_current(&med, [](const cwlb_ctx* c) { return c->last_call_packed; }, 0.0f);
+            if (st == CWLB_OK && med > 0.0f && med < base) base = med;
+            else ctx->sched_tiling = 0;
+        }
         // Column phases, where they can pay: H beyond the Infinity Cache
         // (>= 512 MB) and rows of 64 nonzeros or more on average (each
         // phase reads and writes C once).  8, 12 and 16 phases, each with
@@ -717,24 +747,35 @@ cwlb_status cwlb_ctx_tune_schedule(cwlb_ctx* ctx, const int32_t* row_ptr, const 
             st = time_current(&base, nullptr, 0.0f);
             const long long hot_kept = ctx->sched_hot_bytes;
             const int occ_kept = ctx->sched_occupancy;
-            int best_p = 0, best_pm = best.first, best_psl = best.second;
+            const int tiling_kept = ctx->sched_tiling;
+            int best_p = 0, best_pm = best.first, best_psl = best.second, best_pt = 0;
+            ctx->sched_hot_bytes = 0;
+            ctx->sched_occupancy = 0;
             for (int P : {8, 12, 16}) {
                 for (int sl : {1, 2, 4, 8}) {
                     if (K / 4 < sl || (K / 4 + sl - 1) / sl > 64) continue;
                     for (int m : {16, 32, 64}) {
-                        if (st != CWLB_OK) break;
-                        ctx->sched_phases = P;
-                        ctx->sched_slices = sl;
-                        ctx->sched_tasks_per_wave = m;
-                        float med = 0.0f;
-                        st = time_current(&med, [](const cwlb_ctx* c) {
-                            return c->last_launch.column_phases > 1;
-                        }, base * 1.1f);
-                        if (st == CWLB_OK && med > 0.0f && med < base) {
-                            base = med;
-                            best_p = P;
-                            best_pm = m;
-                            best_psl = sl;
+                        // Each with power-of-two slots, then packed slots
+                        // where those differ.
+                        for (int til : {0, 2}) {
+                            if (st != CWLB_OK) break;
+                            ctx->sched_phases = P;
+                            ctx->sched_slices = sl;
+                            ctx->sched_tasks_per_wave = m;
+                            ctx->sched_tiling = til;
+                            float med = 0.0f;
+                            st = time_current(&med, til == 0 ? +[](const cwlb_ctx* c) {
+                                return c->last_launch.column_phases > 1;
+                            } : +[](const cwlb_ctx* c) {
+                                return c->last_launch.column_phases > 1 && c->last_call_packed;
+                            }, base * 1.1f);
+                            if (st == CWLB_OK && med > 0.0f && med < base) {
+                                base = med;
+                                best_p = P;
+                                best_pm = m;
+                                best_psl = sl;
+                                best_pt = til;
+                            }
                         }
                     }
                 }
@@ -744,11 +785,11 @@ cwlb_status cwlb_ctx_tune_schedule(cwlb_ctx* ctx, const int32_t* row_ptr, const 
                 // The phased kernel takes neither hints nor the variant.
                 best.first = best_pm;
                 best.second = best_psl;
-                ctx->sched_hot_bytes = 0;
-                ctx->sched_occupancy = 0;
+                ctx->sched_tiling = best_pt;
             } else {
                 ctx->sched_hot_bytes = hot_kept;
                 ctx->sched_occupancy = occ_kept;
+                ctx->sched_tiling = tiling_kept;
             }
             ctx->sched_tasks_per_wave = best.first;
             ctx->sched_slices = best.second;

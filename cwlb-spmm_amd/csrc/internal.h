@@ -37,6 +37,7 @@ struct cwlb_ctx {
     int sched_order = 0;
     int sched_xcd = 0;
     int sched_occupancy = 0;  // 0 standard kernel, 6 the 6-waves-per-SIMD variant
+    int sched_tiling = 0;     // 0 automatic, 1 power-of-two slots, 2 packed slots
     // Grow-only device buffers for the run order: keys, sorted keys, the
     // order itself and the sort's temporary storage.
     unsigned* d_run_keys = nullptr;
@@ -77,6 +78,7 @@ struct cwlb_ctx {
     unsigned hint_theta = 0;
     bool hint_any_cold = false;
     bool last_call_hinted = false;  // the last aggregation launch used hints
+    bool last_call_packed = false;  // the last aggregation launch used packed slots
     // Column phases (0 or 1 = none): grow-only buffers that each phased call
     // rewrites -- the P - 1 interior row bounds (P - 1 arrays of n_rows
     // ints) and the band-sorted copy of the column and value arrays -- and

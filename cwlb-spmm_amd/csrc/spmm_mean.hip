@@ -972,6 +972,9 @@ struct Plan {
     long long grid;        // launched blocks
     bool ordered;          // runs execute sorted by output row id
     bool o6;               // the 6-waves-per-SIMD variant
+    bool packed;           // packed slots (G lanes x R vectors, see pick_tiling)
+    int G;                 // lanes per slot of the launch
+    int R;                 // vectors per lane and pass of the launch
     const int* order;      // that order (device), set at launch
     const unsigned long long* hints;  // cold-column bits (device) or null
     int phases;            // column phases (1 = none)
@@ -1053,10 +1056,47 @@ int dispatch_o6(hipStream_t st, const SpmmArgs& a, const Plan& p, int* status, i
     }
 }
 
+// Packed slots (16-byte lanes): G lanes of R = 3 or 5 vectors each, for the
+// slices those cover with fewer idle lanes than one vector per lane in a
+// power-of-two slot.  Slices of at most 64 vectors (all variants) use
+// G x R in {4x3, 4x5, 8x3, 8x5, 16x3}; wider ones (plain kernel only) also
+// 16x5, 32x3 and 32x5 (64x3 and 64x5 are the SL = 1 wide tilings).
+template <int SL, bool HN, bool PH>
+int dispatch_packed(hipStream_t st, const SpmmArgs& a, const Plan& p, int* status)
+{
+    switch (p.G * 10 + p.R) {
+    case 43: return launch_main<4, 4, 3, SL, HN, false, PH>(st, a, p, status);
+    case 45: return launch_main<4, 4, 5, SL, HN, false, PH>(st, a, p, status);
+    case 83: return launch_main<4, 8, 3, SL, HN, false, PH>(st, a, p, status);
+    case 85: return launch_main<4, 8, 5, SL, HN, false, PH>(st, a, p, status);
+    default: return launch_main<4, 16, 3, SL, HN, false, PH>(st, a, p, status);
+    }
+}
+
+template <int SL>
+int dispatch_packed_wide(hipStream_t st, const SpmmArgs& a, const Plan& p, int* status)
+{
+    switch (p.G * 10 + p.R) {
+    case 165: return launch_main<4, 16, 5, SL>(st, a, p, status);
+    case 323: return launch_main<4, 32, 3, SL>(st, a, p, status);
+    case 325: return launch_main<4, 32, 5, SL>(st, a, p, status);
+    case 643: return launch_main<4, 64, 3, SL>(st, a, p, status);
+    case 645: return launch_main<4, 64, 5, SL>(st, a, p, status);
+    default: return dispatch_packed<SL, false, false>(st, a, p, status);
+    }
+}
+
 template <int VEC, int SL>
 int dispatch_width(hipStream_t st, const SpmmArgs& a, const Plan& p, int* status)
 {
     const int F = (a.K / VEC + SL - 1) / SL;  // vectors of the widest slice
+    if constexpr (VEC == 4) {
+        if (p.packed) {
+            if (p.phases > 1) return dispatch_packed<SL, false, true>(st, a, p, status);
+            if (p.hints) return dispatch_packed<SL, true, false>(st, a, p, status);
+            return dispatch_packed_wide<SL>(st, a, p, status);
+        }
+    }
     if (F <= 64) {
         int G = 1;
         while (G < F) G <<= 1;
@@ -1121,6 +1161,55 @@ int pick_vec(const SpmmArgs& a)
     if (a.K % 4 == 0 && h % 16 == 0 && c % 16 == 0) return 4;
     if (a.K % 2 == 0 && h % 8 == 0 && c % 8 == 0) return 2;
     return 1;
+}
+
+// The slot tiling of a slice of F vectors: G lanes per slot, R vectors per
+// lane and pass, ceil(F / (G R)) passes over the row's nonzeros.
+// Power-of-two slots: G the smallest power of two >= F with R = 1
+// (F <= 64); wider slices G = 64 and, without feature slices,
+// R = ceil(F / 64) up to 8.  Packed slots: for F <= 64, of those and the
+// one-pass G x R in {4x3, 4x5, 8x3, 8x5, 16x3}, the fewest vector loads per
+// nonzero (G R: the fewest idle lanes), the smaller R on a tie; for wider
+// slices, of those and 16x5, 32x3, 32x5, 64x3 and 64x5, the fewest passes
+// (each pass reads the row's indices again), then the fewest loads, then
+// the smaller R.  wide: slices above 64 vectors may use the wide tilings
+// (not under hints or column phases).
+void pick_tiling(int F, int SL, bool packed, bool wide, int* G_out, int* R_out)
+{
+    int G = 64, R = 1;
+    if (F <= 64) {
+        G = 1;
+        while (G < F) G <<= 1;
+    } else if (SL == 1) {
+        R = std::min((F + 63) / 64, 8);
+    }
+    if (packed) {
+        auto passes = [F](int g, int r) { return (F + g * r - 1) / (g * r); };
+        auto better = [&](int g, int r) {
+            const long long c = static_cast<long long>(passes(g, r)) * g * r;
+            const long long c0 = static_cast<long long>(passes(G, R)) * G * R;
+            if (passes(g, r) != passes(G, R)) return passes(g, r) < passes(G, R);
+            if (c != c0) return c < c0;
+            return r < R;
+        };
+        const int narrow[5][2] = {{4, 3}, {4, 5}, {8, 3}, {8, 5}, {16, 3}};
+        const int wide_t[5][2] = {{16, 5}, {32, 3}, {32, 5}, {64, 3}, {64, 5}};
+        if (F <= 64) {
+            for (const auto& t : narrow)
+                if (t[0] * t[1] >= F && better(t[0], t[1])) {
+                    G = t[0];
+                    R = t[1];
+                }
+        } else if (wide) {
+            for (const auto& t : wide_t)
+                if ((t[0] < 64 || SL == 1) && better(t[0], t[1])) {
+                    G = t[0];
+                    R = t[1];
+                }
+        }
+    }
+    *G_out = G;
+    *R_out = R;
 }
 
 // Automatic schedule (the context's settings override each choice):
@@ -1197,6 +1286,12 @@ Plan make_plan(const cwlb_ctx* ctx, const SpmmArgs& a, bool per_task)
     p.first = 1;
     p.seq = 0;
     p.write_empty = 1;
+    // Packed slots: 16-byte lanes, not with the occupancy variant or one
+    // task per wave.  The tiling is settled at launch (hints and phases
+    // restrict it).
+    p.packed = !per_task && ctx->sched_tiling == 2 && p.vec == 4 && !p.o6;
+    p.G = 0;
+    p.R = 0;
     return p;
 }
 
@@ -1271,12 +1366,23 @@ cwlb_status launch_spmm_mean(cwlb_ctx* ctx, const SpmmArgs& a, bool zero_all, bo
     ctx->last_launch.grid_blocks = a.n_tasks > 0 && a.K > 0 ? p.grid : 0;
     ctx->last_launch.max_waves_per_cu = 0;
     ctx->last_launch.column_phases = p.phases;
+    {
+        const int F = (a.K / p.vec + p.sl - 1) / p.sl;
+        pick_tiling(F, p.sl, p.packed, !p.hints && p.phases == 1, &p.G, &p.R);
+        // A packed pick that is no different launches the standard tilings.
+        int G1 = 0, R1 = 0;
+        pick_tiling(F, p.sl, false, false, &G1, &R1);
+        if (p.G == G1 && p.R == R1) p.packed = false;
+        ctx->last_call_packed = p.packed && work;
+        ctx->last_launch.slot_lanes = p.G;
+        ctx->last_launch.lane_vectors = p.R;
+    }
     // A phased call sorts each row's nonzeros by band into the context's
     // copy, and always runs the clearing pass: it also checks the chain.
     if (p.phases > 1) {
         const cwlb_status s =
             launch_band_sort(st, a.row_ptr, a.col_idx, a.val, a.n_rows, a.nnz, a.h_rows,
-                             p.phases, ph_arr.bounds, ph_arr.col, ph_arr.val);
+                             p.phases, ph_arr.bounds, ph_arr.col, ph_arr.val, ctx->d_status + 1);
         if (s != CWLB_OK) return s;
     }
     if ((!zero_all || p.phases > 1) && work) {

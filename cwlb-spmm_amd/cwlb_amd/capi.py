@@ -27,6 +27,7 @@ EXPORTS = [
     "cwlb_ctx_set_locality", "cwlb_ctx_set_cache_hints", "cwlb_ctx_get_cache_hints",
     "cwlb_ctx_last_launch", "cwlb_ctx_set_occupancy", "cwlb_ctx_get_occupancy",
     "cwlb_ctx_set_column_phases", "cwlb_ctx_get_column_phases", "cwlb_column_phase_sort",
+    "cwlb_ctx_set_lane_tiling", "cwlb_ctx_get_lane_tiling",
     "cwlb_ctx_tune_schedule",
     "cwlb_spmm_mean_f32", "cwlb_spmm_mean_f32_large_k", "cwlb_spmm_mean_f32_host",
     "cwlb_spmm_mean_f32_noalloc",
@@ -83,7 +84,8 @@ class LaunchInfo(C.Structure):
                 ("run_order", C.c_int32), ("xcd_blocks", C.c_int32),
                 ("cache_hints", C.c_int32), ("vector_width", C.c_int32),
                 ("waves_per_simd", C.c_int32), ("max_waves_per_cu", C.c_int32),
-                ("column_phases", C.c_int32), ("grid_blocks", C.c_int64)]
+                ("column_phases", C.c_int32), ("slot_lanes", C.c_int32),
+                ("grid_blocks", C.c_int64), ("lane_vectors", C.c_int32)]
 
 
 class DeviceInfo(C.Structure):
@@ -143,6 +145,8 @@ def lib():
         L.cwlb_ctx_get_occupancy.argtypes = [vp, C.POINTER(i32)]
         L.cwlb_ctx_set_column_phases.argtypes = [vp, i32]
         L.cwlb_ctx_get_column_phases.argtypes = [vp, C.POINTER(i32)]
+        L.cwlb_ctx_set_lane_tiling.argtypes = [vp, i32]
+        L.cwlb_ctx_get_lane_tiling.argtypes = [vp, C.POINTER(i32)]
         L.cwlb_column_phase_sort.argtypes = [vp, vp, vp, vp, i32, i64, i64, i32, vp, vp, vp]
         L.cwlb_ctx_tune_schedule.argtypes = [vp, vp, vp, vp, vp, i32, i64, vp, i64, i32, vp, i64,
                                              vp, i32, C.POINTER(i32), C.POINTER(i32), vp]
@@ -346,6 +350,14 @@ class Context:
     def occupancy(self):
         v = i32()
         check(lib().cwlb_ctx_get_occupancy(self.h, C.byref(v)))
+        return v.value
+
+    def set_lane_tiling(self, tiling=0):
+        check(lib().cwlb_ctx_set_lane_tiling(self.h, int(tiling)))
+
+    def lane_tiling(self):
+        v = i32()
+        check(lib().cwlb_ctx_get_lane_tiling(self.h, C.byref(v)))
         return v.value
 
     def set_column_phases(self, phases=0):

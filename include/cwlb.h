@@ -162,6 +162,27 @@ cwlb_status cwlb_ctx_get_cache_hints(cwlb_ctx* ctx, int64_t* hot_bytes);
 cwlb_status cwlb_ctx_set_occupancy(cwlb_ctx* ctx, int32_t waves_per_simd);
 cwlb_status cwlb_ctx_get_occupancy(cwlb_ctx* ctx, int32_t* waves_per_simd);
 
+/* Lane tiling of later SpMM calls.  A feature slice of F vectors (4 floats
+ * each) is covered by slots of G lanes, each lane holding R vectors per
+ * pass; a wave has 64 / G slots, each working on its own row (short rows)
+ * or nonzero (long rows).  1: power-of-two slots, G the smallest power of
+ * two >= F and R = 1 (F <= 64; wider slices G = 64, R = ceil(F / 64) up to 8
+ * without feature slices, else G = 64 in several passes).  2: packed slots,
+ * G x R also in {4x3, 4x5, 8x3, 8x5, 16x3} (wider slices, without cache
+ * hints or column phases: 16x5, 32x3, 32x5, 64x3, 64x5), whichever covers
+ * the slice with the fewest vector loads per nonzero (the fewest idle
+ * lanes), the smaller R on a tie: F = 24 (K = 96) runs in 8-lane slots of 3
+ * vectors instead of 32-lane slots with 8 lanes idle.  Applies with 16-byte
+ * aligned H and C and K a multiple of 4, not with the occupancy variant or
+ * CWLB_SPMM_PER_TASK.  0 = automatic (currently 1).  Results agree within
+ * the float tolerance (each lane still sums its vectors in CSR order, so
+ * rows summed by one slot are unchanged bit for bit).  The reference pads
+ * the row the same way (parallelMatrix.cpp:93-99: a work-group of K
+ * rounded up).  No counterpart in the reference; cwlb_ctx_tune_schedule
+ * tries it. */
+cwlb_status cwlb_ctx_set_lane_tiling(cwlb_ctx* ctx, int32_t tiling);
+cwlb_status cwlb_ctx_get_lane_tiling(cwlb_ctx* ctx, int32_t* tiling);
+
 /* Column phases of later SpMM calls on this context.  phases = 0 or 1 (the
  * default): one pass.  phases = P in [2, 64]: the task list is executed P
  * times, pass p gathering only the nonzeros whose column c has
@@ -230,8 +251,10 @@ typedef struct cwlb_launch_info {
     int32_t column_phases;   /* column phases planned (1 = none; a task list
                                 that is not a chain runs unphased all the
                                 same, see cwlb_ctx_set_column_phases) */
+    int32_t slot_lanes;      /* lanes per row slot (see cwlb_ctx_set_lane_tiling) */
     int64_t grid_blocks;     /* work-groups of the aggregation kernel (per
                                 phase) */
+    int32_t lane_vectors;    /* vectors each lane of a slot holds per pass */
 } cwlb_launch_info;
 cwlb_status cwlb_ctx_last_launch(cwlb_ctx* ctx, cwlb_launch_info* out);
 
@@ -340,15 +363,19 @@ cwlb_status cwlb_spmm_mean_f32_large_k(cwlb_ctx* ctx, const int32_t* row_ptr,
  * tasks per wave returned can be 1); then with cache hints of 24, 48 and
  * 96 MB (cwlb_ctx_set_cache_hints), the fastest kept on the context (0 =
  * none; read it with cwlb_ctx_get_cache_hints); then the standard kernel
- * again with those hints when the variant was kept; then, when H holds at
- * least 512 MB, K is a multiple of 4 and rows average 64 nonzeros or more,
- * with 8, 12 and 16 column phases (cwlb_ctx_set_column_phases) at every
- * slice count they take and 16, 32 or 64 tasks per wave: the fastest is kept
- * when it beats the settings so far (its tasks per wave and slices are
- * then the ones returned; read the phases with
- * cwlb_ctx_get_column_phases), otherwise phases stay off.  In that mode
+ * again with those hints when the variant was kept; then with packed
+ * slots (cwlb_ctx_set_lane_tiling(2), where they change the tiling), kept
+ * when faster; then, when H holds at least 512 MB, K is a multiple of 4 and
+ * rows average 64 nonzeros or more, with 8, 12 and 16 column phases
+ * (cwlb_ctx_set_column_phases) at every slice count they take and 16, 32
+ * or 64 tasks per wave, each with power-of-two and with packed slots: the
+ * fastest is kept when it beats the settings so far (its tasks per wave and
+ * slices are then the ones returned; read the phases with
+ * cwlb_ctx_get_column_phases and the tiling with
+ * cwlb_ctx_get_lane_tiling), otherwise phases stay off.  In that mode
  * every timing before the hint sizes runs without hints, every timing
- * before the occupancy variant with the standard kernel, and every timing
+ * before the occupancy variant with the standard kernel, every timing
+ * before the packed slots with the automatic tiling, and every timing
  * before the phases in one pass, whatever the context held.  C receives
  * the result.  Synchronises.  No counterpart in the reference, whose one task
  * per work-group has nothing to tune; like its S search, it is meant to run

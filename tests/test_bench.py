@@ -83,9 +83,11 @@ def test_schedule_args_fix_the_launch(bench):
              "hot_bytes": 48 << 20, "occupancy": 0}
     args = bench.schedule_args(63, sched)
     assert args == ["--s", "63", "--tasks-per-wave", "64", "--slices", "2", "--run-order", "0",
-                    "--xcd-blocks", "0", "--hot-mb", "48", "--occupancy", "0", "--phases", "0"]
+                    "--xcd-blocks", "0", "--hot-mb", "48", "--occupancy", "0", "--phases", "0",
+                    "--tiling", "0"]
     sched["phases"] = 16
-    assert bench.schedule_args(63, sched)[-2:] == ["--phases", "16"]
+    sched["tiling"] = 2
+    assert bench.schedule_args(63, sched)[-4:] == ["--phases", "16", "--tiling", "2"]
 
 
 def test_counters_per_call(bench):

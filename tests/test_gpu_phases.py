@@ -34,6 +34,7 @@ def reset(gpu_ctx):
     gpu_ctx.set_column_phases(0)
     gpu_ctx.set_schedule(0, 0)
     gpu_ctx.set_locality(0, 0)
+    gpu_ctx.set_lane_tiling(0)
 
 
 def expected_phases(K, SL, P):
@@ -393,8 +394,9 @@ def test_tuner_tries_phases(gpu_ctx, reset):
     m, sl, loc = gpu_ctx.tune_schedule(rp, ci, val, origin, n, n * deg, H, n, K, tasks,
                                        len(tasks_np), C, trials=1, locality=True)
     P = gpu_ctx.column_phases()
-    print(f"tuned m={m} sl={sl} loc={loc} phases={P}", flush=True)
+    print(f"tuned m={m} sl={sl} loc={loc} phases={P} tiling={gpu_ctx.lane_tiling()}", flush=True)
     assert P in (0, 8, 12, 16)
+    assert gpu_ctx.lane_tiling() in (0, 2)
     C.fill_(float("nan"))
     gpu_ctx.spmm(rp, ci, val, origin, n, n * deg, H, n, K, tasks, len(tasks_np), C)
     assert gpu_ctx.last_launch()["column_phases"] == max(P, 1)

@@ -358,6 +358,128 @@ def test_large_k_entry(gpu_ctx, K):
     assert e.value.status == capi.INVALID_ARG
 
 
+def expected_tiling(K, SL, packed, wide):
+    """(slot lanes G, vectors per lane R) of a K-float row in SL slices: the
+    restatement of cwlb_ctx_set_lane_tiling's rule (16-byte lanes)."""
+    F = -(-(K // 4) // SL)
+    if F <= 64:
+        G, R = 1 << max(0, (F - 1).bit_length()), 1
+    else:
+        G, R = 64, (min(-(-F // 64), 8) if SL == 1 else 1)
+    if not packed:
+        return G, R
+
+    def key(g, r):
+        passes = -(-F // (g * r))
+        return passes, passes * g * r, r
+    if F <= 64:
+        cands = [(g, r) for g, r in ((4, 3), (4, 5), (8, 3), (8, 5), (16, 3)) if g * r >= F]
+    elif wide:
+        cands = [(g, r) for g, r in ((16, 5), (32, 3), (32, 5), (64, 3), (64, 5))
+                 if g < 64 or SL == 1]
+    else:
+        cands = []
+    for g, r in cands:
+        if key(g, r) < key(G, R):
+            G, R = g, r
+    return G, R
+
+
+def test_expected_tiling_examples():
+    """The packed tilings the kernel's slices get: K = 96 in 8 x 3, K = 600 in
+    4 slices (38 vectors) in 8 x 5, in 8 slices (19) in 4 x 5, in 2 slices
+    (75) in 16 x 5 and in one (150) in 32 x 5; power-of-two widths keep
+    one vector per lane."""
+    assert expected_tiling(96, 1, True, True) == (8, 3)
+    assert expected_tiling(96, 1, False, True) == (32, 1)
+    assert expected_tiling(600, 4, True, True) == (8, 5)
+    assert expected_tiling(600, 8, True, True) == (4, 5)
+    assert expected_tiling(600, 2, True, True) == (16, 5)
+    assert expected_tiling(600, 1, True, True) == (32, 5)
+    assert expected_tiling(600, 1, False, True) == (64, 3)
+    assert expected_tiling(600, 4, True, False) == (8, 5)  # hints and phases: one pass
+    assert expected_tiling(2052, 1, True, True) == (64, 5)  # 513 vectors: 2 x 320, not 2 x 512
+    assert expected_tiling(128, 2, True, True) == (16, 1)
+    assert expected_tiling(64, 1, True, True) == (16, 1)
+
+
+# (K, feature slices, variant): widths whose slices the packed tiling
+# covers with fewer idle lanes (and power-of-two ones it leaves), with
+# slices, cache hints and column phases.
+PACKED_CASES = [(K, sl, v) for K in (12, 20, 36, 48, 96, 100, 152, 300, 600, 1000)
+                for sl in (1, 2, 4, 8) for v in ("plain", "hints", "phases")
+                if K // 4 >= sl]
+_PACKED = {}
+
+
+def _packed_problem(K):
+    """The graph, task list, features and oracle results of width K (kept
+    for the cases of one K, which run one after the other)."""
+    if K not in _PACKED:
+        _PACKED.clear()
+        g = workloads.small(4, seed=5)
+        H = synth.features(g.n, K, 7)
+        p = problem(g, SKEWED_COSTS, 8)
+        _PACKED[K] = (g, H, p, oracle_pair(p, g, H))
+    return _PACKED[K]
+
+
+@pytest.mark.parametrize("K,sl,variant", PACKED_CASES)
+def test_packed_lane_tiling(gpu_ctx, K, sl, variant):
+    """Packed slots (cwlb_ctx_set_lane_tiling(2)) against the oracle in
+    reference order and the fp64 closed form, with the tiling the launch
+    reports checked against the rule's restatement."""
+    g, H, p, (ref32, ref64) = _packed_problem(K)
+    gpu_ctx.set_schedule(8, sl)
+    gpu_ctx.set_lane_tiling(2)
+    gpu_ctx.set_cache_hints(1 << 16 if variant == "hints" else 0)
+    gpu_ctx.set_column_phases(5 if variant == "phases" else 0)
+    try:
+        got, _ = run_gpu(gpu_ctx, p, H)
+        info = gpu_ctx.last_launch()
+    finally:
+        gpu_ctx.set_schedule(0, 0)
+        gpu_ctx.set_lane_tiling(0)
+        gpu_ctx.set_cache_hints(0)
+        gpu_ctx.set_column_phases(0)
+    wide = info["cache_hints"] == 0 and info["column_phases"] == 1
+    assert (info["slot_lanes"], info["lane_vectors"]) == expected_tiling(K, sl, True, wide), info
+    if variant == "phases" and -(-(K // 4) // sl) <= 64:
+        assert info["column_phases"] == 5, info
+    check(got, ref32)
+    check(got, ref64)
+
+
+@pytest.mark.parametrize("K", [1100, 2052, 4100])
+def test_packed_lane_tiling_large_k(gpu_ctx, K):
+    """The large-K entry with packed slots (K = 2,052: 513 vectors in two
+    passes of 64 x 5 instead of 64 x 8)."""
+    g = workloads.small(1, seed=9)
+    H = synth.features(g.n, K, 5)
+    p = problem(g, UNIT_COSTS, 5)
+    gpu_ctx.set_lane_tiling(2)
+    try:
+        got, _ = run_gpu(gpu_ctx, p, H, large_k=True)
+        info = gpu_ctx.last_launch()
+    finally:
+        gpu_ctx.set_lane_tiling(0)
+    assert (info["slot_lanes"], info["lane_vectors"]) == expected_tiling(
+        K, info["feature_slices"], True, True), info
+    ref32, ref64 = oracle_pair(p, g, H)
+    check(got, ref32)
+    check(got, ref64)
+
+
+def test_lane_tiling_argument(gpu_ctx):
+    for bad in (-1, 3):
+        with pytest.raises(capi.CwlbError) as e:
+            gpu_ctx.set_lane_tiling(bad)
+        assert e.value.status == capi.INVALID_ARG
+    gpu_ctx.set_lane_tiling(1)
+    assert gpu_ctx.lane_tiling() == 1
+    gpu_ctx.set_lane_tiling(0)
+
+
 def test_large_k_entry_rejects_small_k(gpu_ctx):
     g = workloads.small(1, seed=9)
     H = synth.features(g.n, 64, 5)
@@ -1442,6 +1564,7 @@ def test_tune_schedule(gpu_ctx):
         assert loc in ((0, 0), (2, 1), (2, 2))
         assert gpu_ctx.cache_hints() in (0, 24 << 20, 48 << 20, 96 << 20)
         assert gpu_ctx.occupancy() in (0, 6)
+        assert gpu_ctx.lane_tiling() in (0, 2)
         ref32, ref64 = oracle_pair(p, g, H)
         check(C.cpu().numpy(), ref32)
         C.fill_(float("nan"))
@@ -1454,6 +1577,10 @@ def test_tune_schedule(gpu_ctx):
         assert (info["tasks_per_wave"] == m) if m else True, info
         assert info["run_order"] == (2 if loc[0] == 2 else 1), info
         assert info["waves_per_simd"] == gpu_ctx.occupancy(), info
+        wide = info["cache_hints"] == 0 and info["column_phases"] == 1
+        packed = gpu_ctx.lane_tiling() == 2 and info["waves_per_simd"] == 0
+        assert (info["slot_lanes"], info["lane_vectors"]) == expected_tiling(
+            K, info["feature_slices"], packed, wide), info
         with pytest.raises(capi.CwlbError) as e:
             gpu_ctx.tune_schedule(d_rp, d_ci, d_v, d_o, g.n, g.nnz, d_H, g.n, K, d_t,
                                   len(p.tasks), C, trials=0)
@@ -1464,6 +1591,7 @@ def test_tune_schedule(gpu_ctx):
         gpu_ctx.set_cache_hints(0)
         gpu_ctx.set_occupancy(0)
         gpu_ctx.set_column_phases(0)
+        gpu_ctx.set_lane_tiling(0)
 
 
 def test_run_order_reused_across_task_lists(gpu_ctx):
