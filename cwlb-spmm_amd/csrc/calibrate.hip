@@ -13,7 +13,14 @@
 //            same K_block-wide output row, relaxed agent scope (utils.cpp:597-825)
 // Each coefficient is (ns per op per work-item) x 10, as in the reference
 // (utils.cpp:419-421, 522-524, 583-585, 791-806).  The load benchmark groups
-// lanes by the 64-lane wavefront (the reference groups by 32 lanes).
+// lanes by the 64-lane wavefront (the reference groups by 32 lanes) and
+// issues non-temporal loads where the reference's are plain
+// (utils.cpp:470-481).  Each wave reads its one row K times over, and plain
+// loads serve those repeats from the L1 (measured: 0.01100 against 0.01584
+// with non-temporal loads, K = 128, WI = 131072, 512 MB); the aggregation's
+// gathers read a feature row once per nonzero, so they see no such reuse.
+// Partitions from either figure run the aggregation equally fast (R-MAT,
+// Chung-Lu and mesh within 0.2%).
 #include <algorithm>
 #include <cstdio>
 #include <random>
