@@ -15,12 +15,14 @@ as the reference's kernel, leaves the rows without nonzeros at that 0
 (CWLB_SPMM_KEEP_EMPTY_ROWS).
 
 Prints one JSON line: GFLOP/s (2 nnz K / t) as `value`; the aggregation
-kernel's roofline: the L2-to-fabric traffic of one launch (rocprofv3
-FETCH_SIZE + WRITE_SIZE; Infinity Cache hits are included, so it is an
-upper bound on the HBM bytes), measured on a replay of the very launch that
-was timed (child processes running this file with --pmc-child), over the
-kernel's mean event-timed duration, against 8 TB/s, next to the algorithmic
-and compulsory bytes per launch, the L2 hit rate and the occupancy; the CPU
+kernel's roofline: its algorithmic bytes per launch over its mean
+event-timed duration against 8 TB/s (`achieved`, `frac`), and the
+L2-to-fabric traffic of one launch (rocprofv3 FETCH_SIZE + WRITE_SIZE;
+Infinity Cache hits are included, so it is an upper bound on the HBM bytes),
+measured on a replay of the very launch that was timed (child processes
+running this file with --pmc-child), with its rate and fraction
+(`traffic`, `traffic_gbs`, `traffic_frac`), next to the compulsory bytes
+per launch, the L2 hit rate and the occupancy; the CPU
 baseline (the reference kernel's semantics restated with OpenMP, on this
 host's cores, over a sample of the tasks); and the parity of the timed
 launch: the whole of C after the last timed step against the oracle, at
@@ -222,14 +224,21 @@ def pmc_child(args):
 
 
 def roofline_record(counters, err, b_alg, b_min, main_us, launched):
-    """The roofline object: measured traffic per launch (L2-to-fabric bytes,
-    Infinity Cache hits included: an upper bound on the HBM bytes) over the
-    kernel's mean duration against 8 TB/s, with the algorithmic and
-    compulsory bytes beside it."""
+    """The roofline object of the aggregation kernel: `achieved` is its
+    algorithmic bytes per launch (4(N+1) + 8 nnz + 4 nnz K + 4 N K + 4 N + 16 T,
+    every feature-row gather counted as a read) over its mean duration, and
+    `frac` that rate against 8 TB/s; gathers the caches serve let it exceed 1.
+    `traffic` is the measured traffic per launch (L2-to-fabric bytes,
+    Infinity Cache hits included: an upper bound on the HBM bytes), with its
+    rate and fraction beside it (`traffic_gbs`, `traffic_frac`), and the
+    compulsory bytes (CSR, each referenced feature row and C once)."""
     t = main_us * 1e-6
-    rec = {"bound": "hbm", "achieved": None, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": None,
-           "traffic": None, "kernel_us": round(main_us, 2),
-           "algorithmic_bytes": b_alg, "effective_gbs": round(b_alg / t / 1e9, 1),
+    achieved = b_alg / t / 1e9
+    rec = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+           "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel_us": round(main_us, 2),
+           "achieved_kind": "algorithmic bytes per launch (every feature-row gather counted as a "
+                            "read) over the kernel's mean duration",
+           "algorithmic_bytes": b_alg, "traffic_gbs": None, "traffic_frac": None,
            "compulsory_bytes": b_min, "compulsory_gbs": round(b_min / t / 1e9, 1),
            "compulsory_frac": round(b_min / t / 1e9 / HBM_PEAK_GBS, 4),
            "max_waves_per_cu": launched.get("max_waves_per_cu")}
@@ -243,11 +252,11 @@ def roofline_record(counters, err, b_alg, b_min, main_us, launched):
     read_b = k["FETCH_SIZE"] * 1024.0 * fetch_scale
     write_b = k["WRITE_SIZE"] * 1024.0 * write_scale
     traffic = read_b + write_b
-    achieved = traffic / t / 1e9
+    traffic_gbs = traffic / t / 1e9
     hits, misses = k.get("TCC_HIT_sum"), k.get("TCC_MISS_sum")
     rec.update({
-        "achieved": round(achieved, 1), "frac": round(achieved / HBM_PEAK_GBS, 4),
         "traffic": round(traffic), "traffic_read": round(read_b), "traffic_write": round(write_b),
+        "traffic_gbs": round(traffic_gbs, 1), "traffic_frac": round(traffic_gbs / HBM_PEAK_GBS, 4),
         "traffic_kind": "L2-to-fabric bytes (FETCH_SIZE + WRITE_SIZE), Infinity Cache hits "
                         "included: an upper bound on the HBM bytes",
         "kernel": kernel_template(counters["name"]),

@@ -32,9 +32,10 @@ def counters(fetch_kib, write_kib, probe_fetch_kib, probe_write_kib, hits=1.0, m
 
 
 def test_roofline_from_counters(bench):
-    """frac = (FETCH x read scale + WRITE x write scale) / kernel time / 8 TB/s,
-    with the scales from the 1 GiB copy; the algorithmic and compulsory
-    rates beside it; a 4 ms launch moving 24 GB runs at 6 TB/s = 0.75."""
+    """achieved = algorithmic bytes / kernel time, frac = achieved / 8 TB/s
+    (36 GB in 4 ms: 9 TB/s, 1.125); traffic_frac = (FETCH x read scale +
+    WRITE x write scale) / kernel time / 8 TB/s, with the scales from the
+    1 GiB copy (24 GB in 4 ms: 6 TB/s = 0.75); the compulsory rate beside."""
     probe_kib = 1 << 20  # 1 GiB
     # FETCH_SIZE reads half of the copy's bytes: read scale 2; WRITE exact.
     c = counters(fetch_kib=10e9 / 1024 / 2, write_kib=14e9 / 1024, probe_fetch_kib=probe_kib / 2,
@@ -43,9 +44,10 @@ def test_roofline_from_counters(bench):
                                 launched={"max_waves_per_cu": 28})
     assert rec["traffic"] == pytest.approx(24e9)
     assert rec["traffic_read"] == pytest.approx(10e9) and rec["traffic_write"] == pytest.approx(14e9)
-    assert rec["achieved"] == pytest.approx(6000.0) and rec["frac"] == pytest.approx(0.75)
-    assert rec["frac"] == pytest.approx(rec["traffic"] / (rec["kernel_us"] * 1e-6) / 8e12)
-    assert rec["effective_gbs"] == pytest.approx(9000.0)
+    assert rec["traffic_gbs"] == pytest.approx(6000.0) and rec["traffic_frac"] == pytest.approx(0.75)
+    assert rec["traffic_frac"] == pytest.approx(rec["traffic"] / (rec["kernel_us"] * 1e-6) / 8e12)
+    assert rec["achieved"] == pytest.approx(9000.0) and rec["frac"] == pytest.approx(1.125)
+    assert rec["frac"] == pytest.approx(rec["algorithmic_bytes"] / (rec["kernel_us"] * 1e-6) / 8e12)
     assert rec["compulsory_gbs"] == pytest.approx(1200.0)
     assert rec["compulsory_frac"] == pytest.approx(0.15)
     assert rec["l2_hit_rate"] == pytest.approx(0.25)
@@ -57,9 +59,9 @@ def test_roofline_from_counters(bench):
 
 def test_roofline_without_counters(bench):
     rec = bench.roofline_record(None, "rocprofv3 not found", 36e9, 4.8e9, 4000.0, {})
-    assert rec["traffic"] is None and rec["frac"] is None and rec["achieved"] is None
+    assert rec["traffic"] is None and rec["traffic_frac"] is None and rec["traffic_gbs"] is None
     assert rec["counters_error"] == "rocprofv3 not found"
-    assert rec["effective_gbs"] == pytest.approx(9000.0)
+    assert rec["achieved"] == pytest.approx(9000.0) and rec["frac"] == pytest.approx(1.125)
 
 
 def test_counter_csv_reader(bench, tmp_path):
