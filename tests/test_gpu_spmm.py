@@ -1163,7 +1163,8 @@ def test_schedule_and_locality_arguments(gpu_ctx):
 MB = 1 << 20
 # Launch schedules checked at full size, per workload, as
 # (segment-size candidate index, tasks per wave, feature slices, run order,
-# XCD placement, hot-set bytes, waves per SIMD, flags[, column phases]);
+# XCD placement, hot-set bytes, waves per SIMD, flags[, column phases[, lane
+# tiling]]);
 # None = the schedule cwlb_ctx_tune_schedule picks, which is what bench.py
 # times (bench.py also checks the whole C of its own timed launch).  The
 # first R-MAT entries are headline launches of the benchmark (64 tasks per
@@ -1172,8 +1173,10 @@ MB = 1 << 20
 # per wave, 2 slices, 48 MB hints, automatic placement); the mesh entries
 # are the launches its tuner kept
 # (runs by output row, contiguous XCD stretches, the occupancy variant); the
-# SBM's phased entries are its tuner's launch (12 phases, 8 slices) and the
-# best point of a phase sweep in task order (16 phases, 4 slices).
+# SBM's phased entries are its tuner's launches (12 phases, 8 slices; 16
+# phases, 4 slices of packed 8 x 5 slots at S = 110) and other points of
+# the phase sweep (16 phases, 4 slices, in task order; packed at S = 55),
+# and its one-pass launch with packed 32 x 5 slots.
 FULL_LAUNCHES = {
     4: [(0, 64, 2, 1, 1, 48 * MB, 0, 0), (2, 64, 2, 1, 1, 48 * MB, 0, 0),
         (2, 32, 2, 0, 0, 48 * MB, 0, 0), (2, None),
@@ -1185,7 +1188,9 @@ FULL_LAUNCHES = {
     5: [(2, 1, 1, 2, 2, 0, 6, 0), (2, 2, 1, 2, 2, 0, 6, 0), (1, 4, 1, 2, 2, 0, 6, 0),
         (2, None), (2, 0, 0, 0, 0, 0, 0, 0), (2, 0, 0, 0, 0, 0, 0, capi.PER_TASK)],
     3: [(0, 64, 1, 2, 2, 0, 0, 0), (0, None), (0, 0, 0, 0, 0, 0, 0, 0), (2, 8, 1, 2, 2, 0, 0, 0),
-        (1, 64, 8, 2, 2, 0, 0, 0, 12), (1, 16, 4, 1, 1, 0, 0, 0, 16)],
+        (1, 64, 8, 2, 2, 0, 0, 0, 12), (1, 16, 4, 1, 1, 0, 0, 0, 16),
+        (1, 16, 4, 2, 2, 0, 0, 0, 16, 2), (0, 64, 4, 2, 2, 0, 0, 0, 16, 2),
+        (0, 64, 1, 2, 2, 0, 0, 0, 0, 2)],
     2: [(1, 8, 1, 1, 1, 0, 6, 0), (1, None), (2, 0, 0, 0, 0, 0, 0, capi.PER_TASK)],
 }
 
@@ -1241,6 +1246,7 @@ def test_full_size_launches_vs_oracle(gpu_ctx, cfg):
                 gpu_ctx.set_cache_hints(hot)
                 gpu_ctx.set_occupancy(occ)
                 gpu_ctx.set_column_phases(launch[8] if len(launch) > 8 else 0)
+                gpu_ctx.set_lane_tiling(launch[9] if len(launch) > 9 else 0)
             C.fill_(float("nan"))
             gpu_ctx.spmm(*args, flags=flags)
             info = gpu_ctx.last_launch()
@@ -1251,18 +1257,24 @@ def test_full_size_launches_vs_oracle(gpu_ctx, cfg):
                 assert info["feature_slices"] == sl or sl == 0, what
                 assert info["cache_hints"] == int(hot > 0), what
                 assert info["column_phases"] == max(launch[8] if len(launch) > 8 else 1, 1), what
+                wide = info["cache_hints"] == 0 and info["column_phases"] == 1
+                packed = len(launch) > 9 and launch[9] == 2 and info["waves_per_simd"] == 0
+                assert (info["slot_lanes"], info["lane_vectors"]) == expected_tiling(
+                    K, info["feature_slices"], packed, wide), what
             _assert_close_on_device(torch, C, ref_dev, what)
             gpu_ctx.set_schedule(0, 0)
             gpu_ctx.set_locality(0, 0)
             gpu_ctx.set_cache_hints(0)
             gpu_ctx.set_occupancy(0)
             gpu_ctx.set_column_phases(0)
+            gpu_ctx.set_lane_tiling(0)
     finally:
         gpu_ctx.set_schedule(0, 0)
         gpu_ctx.set_locality(0, 0)
         gpu_ctx.set_cache_hints(0)
         gpu_ctx.set_occupancy(0)
         gpu_ctx.set_column_phases(0)
+        gpu_ctx.set_lane_tiling(0)
 
 
 MESH_S_SWEEP = (32, 64, 128, 256, 512)
