@@ -192,6 +192,7 @@ SingleSResult run_single_s(cwlb::Device& queue, const CSR_Order& csr,
     cwlb::check(cwlb_ctx_set_cache_hints(queue.ctx(), 0), "cwlb_ctx_set_cache_hints");
     cwlb::check(cwlb_ctx_set_occupancy(queue.ctx(), 0), "cwlb_ctx_set_occupancy");
     cwlb::check(cwlb_ctx_set_column_phases(queue.ctx(), 0), "cwlb_ctx_set_column_phases");
+    cwlb::check(cwlb_ctx_set_lane_tiling(queue.ctx(), 0), "cwlb_ctx_set_lane_tiling");
     const char* tune_env = std::getenv("CWLB_TUNE_SCHEDULE");
     const bool tune = !(tune_env && std::string(tune_env) == "0");
     if (tune && !tasks.empty() && K > 0) {
@@ -211,6 +212,8 @@ SingleSResult run_single_s(cwlb::Device& queue, const CSR_Order& csr,
                     "cwlb_ctx_get_occupancy");
         cwlb::check(cwlb_ctx_get_column_phases(queue.ctx(), &result.column_phases),
                     "cwlb_ctx_get_column_phases");
+        cwlb::check(cwlb_ctx_get_lane_tiling(queue.ctx(), &result.lane_tiling),
+                    "cwlb_ctx_get_lane_tiling");
     }
 
     const std::string device_name = queue.name();

@@ -77,6 +77,9 @@ struct SingleSResult {
     std::int32_t waves_per_simd = 0;
     // Column phases the timed launches ran with (0 = one pass).
     std::int32_t column_phases = 0;
+    // Lane tiling the timed launches ran with (0 = automatic, 2 = packed
+    // slots; see cwlb_ctx_set_lane_tiling).
+    std::int32_t lane_tiling = 0;
 };
 
 // Builds the tasks for S (on the GPU, identical to the host partition), then

@@ -321,7 +321,8 @@ int run(int argc, char** argv)
                   << r.timed_samples_us.size() << " capacity " << r.capacity << " schedule "
                   << r.schedule[0] << ',' << r.schedule[1] << ',' << r.schedule[2] << ','
                   << r.schedule[3] << " hints " << r.cache_hint_bytes << " occupancy "
-                  << r.waves_per_simd << " phases " << r.column_phases << "\n";
+                  << r.waves_per_simd << " phases " << r.column_phases << " tiling "
+                  << r.lane_tiling << "\n";
         write_dense(argv[11], r.output);
     } else if (cmd == "load") {
         need(2);

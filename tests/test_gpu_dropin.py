@@ -245,14 +245,15 @@ def test_dropin_run_single_s(tmp_path, tune):
     assert float(rec["average"]) > 0 and rec["samples"] == "50"
     m, sl, run_order, xcd = map(int, rec["schedule"].split(","))
     if tune == "0":
-        assert (m, sl, run_order, xcd, rec["hints"], rec["occupancy"], rec["phases"]) == (
-            0, 0, 0, 0, "0", "0", "0")
+        assert (m, sl, run_order, xcd, rec["hints"], rec["occupancy"], rec["phases"],
+                rec["tiling"]) == (0, 0, 0, 0, "0", "0", "0", "0")
     else:
         assert m in (0, 1, 2, 4, 8, 16, 32, 64) and sl in (0, 1, 2, 4)
         assert (run_order, xcd) in ((0, 0), (2, 1), (2, 2))
         assert int(rec["hints"]) in (0, 24 << 20, 48 << 20, 96 << 20)
         assert rec["occupancy"] in ("0", "6")
         assert rec["phases"] == "0"  # a 128 KB feature matrix: phases cannot pay
+        assert rec["tiling"] in ("0", "2")
     assert len([ln for ln in out.splitlines() if ln.startswith("[Iteration ")]) == 50
     cap = capi.capacity_from_s(S, SKEWED_COSTS)
     tasks = oracle.partition(order[1], SKEWED_COSTS, cap)
