@@ -1277,6 +1277,46 @@ def test_full_size_launches_vs_oracle(gpu_ctx, cfg):
         gpu_ctx.set_lane_tiling(0)
 
 
+@pytest.mark.parametrize("K", [32, 64, 96])
+def test_full_rmat_feature_widths_vs_oracle(gpu_ctx, K):
+    """The full R-MAT graph at the paper's other feature widths (32, 64 and
+    96; 128 is the headline above), S = 63 with the committed cost file:
+    the schedule cwlb_ctx_tune_schedule keeps, and the same schedule with
+    packed slots (at K = 96, 8 lanes x 3 vectors instead of 32-lane slots),
+    each on the whole of C against the reference-order oracle
+    (parallelMatrix.cpp:148-236) at 1e-5 relative / 1e-6 absolute."""
+    torch = torch_mod()
+    g = workloads.graph(4)
+    costs = capi.read_costs(paths.COST_FILE)
+    p = problem(g, costs, workloads.candidate_s(g.nnz, 256)[1])
+    H = torch.empty((g.n, K), dtype=torch.float32, device="cuda")
+    gpu_ctx.fill_features(H, g.n, K, workloads.FEATURE_SEED)
+    ref_dev = torch.from_numpy(oracle.spmm_mean_f32_omp(
+        p.row_ptr, p.col_idx, p.val, p.origin, synth.features(g.n, K, workloads.FEATURE_SEED),
+        p.tasks)).cuda()
+    d = [dev(x) for x in (p.row_ptr, p.col_idx, p.val, p.origin)]
+    d_t = dev(np.ascontiguousarray(p.tasks, np.int32).reshape(-1))
+    C = torch.empty((g.n, K), dtype=torch.float32, device="cuda")
+    args = (d[0], d[1], d[2], d[3], g.n, g.nnz, H, g.n, K, d_t, len(p.tasks), C)
+    try:
+        gpu_ctx.tune_schedule(*args, trials=3, locality=True)
+        for tiling in (gpu_ctx.lane_tiling(), 2):
+            gpu_ctx.set_lane_tiling(tiling)
+            C.fill_(float("nan"))
+            gpu_ctx.spmm(*args)
+            info = gpu_ctx.last_launch()
+            what = f"rmat K={K} S={p.S} tiling={tiling} ran={info}"
+            print(what, flush=True)
+            _assert_close_on_device(torch, C, ref_dev, what)
+    finally:
+        gpu_ctx.set_schedule(0, 0)
+        gpu_ctx.set_locality(0, 0)
+        gpu_ctx.set_cache_hints(0)
+        gpu_ctx.set_occupancy(0)
+        gpu_ctx.set_column_phases(0)
+        gpu_ctx.set_lane_tiling(0)
+
+
 MESH_S_SWEEP = (32, 64, 128, 256, 512)
 
 
