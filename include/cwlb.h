@@ -420,6 +420,9 @@ cwlb_status cwlb_spmm_mean_f32_host(cwlb_ctx* ctx, const int32_t* row_ptr,
  * input is too large for it.  synchronize != 0: the call waits for the
  * stream and reports a bad column index, origin entry or row offset as
  * CWLB_INVALID_ARG; 0: asynchronous, such entries are skipped unreported.
+ * On a stream under graph capture synchronize must be 0: a call with
+ * synchronize != 0 there returns CWLB_INVALID_ARG before enqueueing
+ * anything, so the capture stays valid.
  * All calls on one GPU share that status word, which each call resets:
  * calls that overlap on one GPU (different streams) may report each
  * other's errors. */
