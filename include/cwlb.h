@@ -99,8 +99,10 @@ cwlb_status cwlb_ctx_destroy(cwlb_ctx* ctx);
 /* Later calls run on `stream`.  The new stream first waits for all work
  * enqueued on the old one so far (an event recorded there), because calls
  * still running on the old stream may read the context's own buffers that a
- * call on the new one rewrites.  Not done when either stream is under graph
- * capture: ordering against a captured graph is then the caller's. */
+ * call on the new one rewrites; so the old stream must not have been
+ * destroyed yet (switch away from a stream before destroying it).  Not done
+ * when either stream is under graph capture: ordering against a captured
+ * graph is then the caller's. */
 cwlb_status cwlb_ctx_set_stream(cwlb_ctx* ctx, void* stream);
 /* Waits for the context's stream; then reports, as CWLB_INVALID_ARG, a bad
  * column index, origin entry or row offset that the last aggregation met
