@@ -1,7 +1,7 @@
 """Seeded random cross-product of graph family, K, S, costs and launch
 schedule (run length, feature slices, run order, XCD placement, cache hints,
-occupancy variant, column phases, flags, feature-view alignment) against the
-oracle.
+occupancy variant, column phases, lane tiling, flags, feature-view
+alignment) against the oracle.
 
 The structured tests in test_gpu_spmm.py cover each setting on fixed graphs;
 these cases draw combinations that no structured test names, with the same
@@ -18,6 +18,7 @@ import pytest
 import oracle
 from conftest import SKEWED_COSTS, UNIT_COSTS
 from cwlb_amd import capi, synth, workloads
+from test_gpu_spmm import expected_tiling
 
 pytestmark = pytest.mark.gpu
 
@@ -50,6 +51,7 @@ def draw_case(i):
         # depend on it
         "phases": [0, 0, 2, 5, 16][int(np.random.default_rng(5000 + i).integers(5))],
         "keep_empty": bool(np.random.default_rng(7000 + i).integers(3) == 0),
+        "tiling": [0, 0, 2][int(np.random.default_rng(9000 + i).integers(3))],
     }
 
 
@@ -90,6 +92,7 @@ def test_random_schedule_case(gpu_ctx, i):
     gpu_ctx.set_cache_hints(c["hot_rows"] * 4 * K)
     gpu_ctx.set_occupancy(c["occupancy"])
     gpu_ctx.set_column_phases(c["phases"])
+    gpu_ctx.set_lane_tiling(c["tiling"])
     flags = c["flags"] | (capi.KEEP_EMPTY_ROWS if c["keep_empty"] else 0)
     try:
         gpu_ctx.spmm(d_rp, d_ci, d_v, d_o, g.n, g.nnz, d_H, g.n, K, d_t, len(p.tasks), C,
@@ -101,6 +104,7 @@ def test_random_schedule_case(gpu_ctx, i):
         gpu_ctx.set_cache_hints(0)
         gpu_ctx.set_occupancy(0)
         gpu_ctx.set_column_phases(0)
+        gpu_ctx.set_lane_tiling(0)
 
     ref = oracle.spmm_mean_f32(p.row_ptr, p.col_idx, p.val, p.origin, H, p.tasks)
     if not c["flags"] & capi.ZERO_OUTPUT:
@@ -144,6 +148,11 @@ def test_random_schedule_case(gpu_ctx, i):
     assert info["waves_per_simd"] == (6 if o6 else 0), (info, c)
     if phased:
         assert info["cache_hints"] == 0, (info, c)
+    if K and len(p.tasks):
+        packed = c["tiling"] == 2 and not per_task and expect_vec == 4 and not o6
+        wide = info["cache_hints"] == 0 and info["column_phases"] == 1
+        assert (info["slot_lanes"], info["lane_vectors"]) == expected_tiling(
+            K, info["feature_slices"], packed, wide, vec=expect_vec), (info, c)
 
 
 N_ENTRY_CASES = 64

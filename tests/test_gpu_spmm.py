@@ -358,10 +358,11 @@ def test_large_k_entry(gpu_ctx, K):
     assert e.value.status == capi.INVALID_ARG
 
 
-def expected_tiling(K, SL, packed, wide):
-    """(slot lanes G, vectors per lane R) of a K-float row in SL slices: the
-    restatement of cwlb_ctx_set_lane_tiling's rule (16-byte lanes)."""
-    F = -(-(K // 4) // SL)
+def expected_tiling(K, SL, packed, wide, vec=4):
+    """(slot lanes G, vectors per lane R) of a K-float row in SL slices of
+    vec-float vectors: the restatement of cwlb_ctx_set_lane_tiling's rule
+    (packed slots take 16-byte lanes only)."""
+    F = -(-(K // vec) // SL)
     if F <= 64:
         G, R = 1 << max(0, (F - 1).bit_length()), 1
     else:
