@@ -7,6 +7,7 @@
 #include <thread>
 #include <vector>
 
+#include "host_threads.h"
 #include "internal.h"
 
 namespace cwlb {
@@ -112,32 +113,6 @@ cwlb_status run_spmm(cwlb_ctx* ctx, const SpmmArgs& a, uint32_t flags, cwlb_timi
     if (st != CWLB_OK) return st;
     if (timing) return finish_timed(ctx, timing);
     return CWLB_OK;
-}
-
-// fn(begin, end) over [0, n) split into contiguous parts, on up to 8 host
-// threads (one per 8 MiB of work or so), the caller's thread included.
-template <class Fn>
-void parallel_ranges(size_t n, size_t grain, Fn fn)
-{
-    const unsigned hw = std::max(1u, std::thread::hardware_concurrency());
-    const size_t T = std::max<size_t>(1, std::min<size_t>({size_t{8}, hw, n / grain}));
-    if (T == 1) {
-        fn(size_t{0}, n);
-        return;
-    }
-    std::vector<std::thread> pool;
-    pool.reserve(T - 1);
-    for (size_t t = 1; t < T; ++t)
-        pool.emplace_back([&, t] { fn(n * t / T, n * (t + 1) / T); });
-    fn(size_t{0}, n / T);
-    for (auto& th : pool) th.join();
-}
-
-void parallel_copy(void* dst, const void* src, size_t bytes)
-{
-    parallel_ranges(bytes, size_t{8} << 20, [&](size_t b, size_t e) {
-        std::memcpy(static_cast<char*>(dst) + b, static_cast<const char*>(src) + b, e - b);
-    });
 }
 
 // Host-pointer transfers through the context's two pinned staging buffers:
@@ -847,19 +822,10 @@ cwlb_status cwlb_spmm_mean_f32_host(cwlb_ctx* ctx, const int32_t* row_ptr,
     // Host-side validation keeps every device access in bounds.
     if (row_ptr[0] < 0 || row_ptr[n_rows] > nnz)
         return fail(CWLB_INVALID_ARG, "spmm: row_ptr outside [0, nnz]");
-    std::atomic<bool> bad_rp{false}, bad_ci{false};
-    parallel_ranges(static_cast<size_t>(n_rows), size_t{1} << 20, [&](size_t b, size_t e) {
-        bool bad = false;
-        for (size_t r = b; r < e; ++r) bad |= row_ptr[r + 1] < row_ptr[r];
-        if (bad) bad_rp = true;
-    });
-    if (bad_rp) return fail(CWLB_INVALID_ARG, "spmm: row_ptr is not non-decreasing");
-    parallel_ranges(static_cast<size_t>(nnz), size_t{1} << 21, [&](size_t b, size_t e) {
-        bool bad = false;
-        for (size_t j = b; j < e; ++j) bad |= col_idx[j] < 0 || col_idx[j] >= h_rows;
-        if (bad) bad_ci = true;
-    });
-    if (bad_ci) return fail(CWLB_INVALID_ARG, "spmm: column index outside [0, h_rows)");
+    if (!offsets_nondecreasing(row_ptr, n_rows))
+        return fail(CWLB_INVALID_ARG, "spmm: row_ptr is not non-decreasing");
+    if (!columns_in_range(col_idx, nnz, h_rows))
+        return fail(CWLB_INVALID_ARG, "spmm: column index outside [0, h_rows)");
     const bool staged = ensure_staging(ctx);
     DevBuf<int32_t> d_rp, d_ci, d_or;
     DevBuf<float> d_val, d_H, d_C;

@@ -214,3 +214,18 @@ def test_threaded_reorder_under_tsan(tmp_path, shape):
     cap = float(np.frombuffer(raw[:8], np.float64)[0])
     tasks = np.frombuffer(raw[8:], np.int32).reshape(-1, 4)
     assert np.array_equal(tasks, oracle.partition(exp[1], costs, cap))
+
+
+def test_host_pointer_threads_under_tsan():
+    """The host-pointer entry's threaded loops (csrc/host_threads.h: the
+    staged copies in ~8 MiB parts on up to 8 threads, the row-offset and
+    column-index checks with their shared flag) under ThreadSanitizer, on
+    buffers large enough for every thread, with bad entries in one part and
+    in every part (all threads raising the flag at once): no race reported
+    and every answer right.  (The entry itself needs a GPU.)"""
+    path = os.path.join(HERE, "cxx", "bin", "threads_probe_tsan")
+    if not os.path.exists(path):
+        pytest.fail(f"{path} missing: build with __graft_entry__.build()")
+    r = subprocess.run([path], capture_output=True, text=True, env=TSAN_ENV, timeout=600)
+    assert "ThreadSanitizer" not in r.stderr, r.stderr[-4000:]
+    assert r.returncode == 0 and r.stdout.strip() == "OK", (r.returncode, r.stdout, r.stderr[-2000:])
