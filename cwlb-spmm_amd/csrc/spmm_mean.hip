@@ -25,7 +25,10 @@
 //     falls apart into one-task segments, the reference's semantics;
 //   * a row slice of Ks = K / SL floats is covered by a "slot" of G lanes,
 //     each lane holding R vectors of VEC floats (128-bit loads when
-//     K % 4 == 0); a wave has NS = 64 / G slots.  With SL > 1 the feature
+//     K % 4 == 0); a wave has NS = 64 / G slots.  By default G is the
+//     smallest power of two that holds the slice (R = 1); packed slots
+//     (G lanes of 3 or 5 vectors, see pick_tiling) cover slices of other
+//     widths with fewer idle lanes.  With SL > 1 the feature
 //     slices are spread over the XCDs (work-groups are dispatched to the 8
 //     XCDs round-robin), so each XCD's L2 caches one slice of the hot
 //     feature rows and holds SL times as many of them;
